@@ -1,0 +1,112 @@
+/*
+ * selectssm.h — C ABI of the MI355X (gfx950) selective-scan library.
+ *
+ * The reference (ihh/selectssm) is pure JAX/Flax and has no FFI; each entry
+ * point below replaces one reference function on the hot path, named in its
+ * comment as file:line (paths relative to the reference's src/selectssm/).
+ *
+ * Conventions
+ *   - Every buffer is device memory owned by the caller.  The library never
+ *     allocates, never synchronises and only enqueues work on `stream`
+ *     (a hipStream_t passed as void*; NULL means the legacy default stream).
+ *   - Tensor layouts are the reference's: u, delta, y, z, dy, du, ddelta: (B,L,D)
+ *     row-major; A, dA: (D,N); Bc, Cc, dB, dC: (B,L,N); Dskip, dD: (D,).
+ *     delta may be (B,L,1) (desc.delta_broadcast=1, selectssm.py:36, 203-210).
+ *   - I/O element type is desc.dtype (f32 or bf16).  A, Dskip, dA, dD and the
+ *     checkpoints are always f32; the recurrent state and every accumulator
+ *     are f32.
+ *   - Return 0 on success, a nonzero SSM_ERR_* code otherwise; the message is
+ *     available from ssm_last_error() on the calling thread.  Nothing aborts.
+ *   - Functions are reentrant.  Calls on different streams do not share state.
+ */
+#ifndef SELECTSSM_H
+#define SELECTSSM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SSM_ABI_VERSION 1
+
+/* error codes */
+#define SSM_OK 0
+#define SSM_ERR_INVALID 1     /* bad shape, pointer or flag */
+#define SSM_ERR_UNSUPPORTED 2 /* valid request this build does not implement */
+#define SSM_ERR_HIP 3         /* HIP runtime error (launch failure, ...) */
+
+/* desc.dtype */
+#define SSM_F32 0
+#define SSM_BF16 1
+
+/* desc.flags */
+#define SSM_REVERSE 1u    /* SelectiveSSM(reverse=True): y written at L-1-t (selectssm.py:167-168, 230-231) */
+#define SSM_COMPLEMENT 2u /* with REVERSE: channel also mirrored, D-1-d (rcps.py:10-13) */
+#define SSM_SKIP 4u       /* y += u*Dskip with u in the scan domain (selectssm.py:238) */
+#define SSM_GATE 8u       /* y *= silu(z) (BidirectionalMamba, selectssm.py:335-336) */
+
+typedef struct ssm_desc {
+  int64_t batch;          /* B */
+  int64_t seqlen;         /* L */
+  int64_t dim;            /* D (channels, D_inner) */
+  int64_t dstate;         /* N, 1..32 */
+  int32_t dtype;          /* SSM_F32 or SSM_BF16 for u, delta, Bc, Cc, z, y, dy, du, ddelta, dB, dC, dz */
+  uint32_t flags;         /* SSM_REVERSE | SSM_COMPLEMENT | SSM_SKIP | SSM_GATE */
+  int32_t delta_broadcast;/* 1: delta is (B,L,1) and shared by all channels */
+  int32_t reserved;       /* must be 0 */
+} ssm_desc_t;
+
+/* Version of this ABI (SSM_ABI_VERSION). */
+int ssm_abi_version(void);
+
+/* Thread-local text of the last error on this thread ("" if none). */
+const char* ssm_last_error(void);
+
+/* Bytes of the forward checkpoint buffer `ckpt` (states entering each block of
+ * the scan's time axis), needed by ssm_bwd.  Returns 0 for an invalid desc. */
+size_t ssm_ckpt_bytes(const ssm_desc_t* desc);
+
+/* Bytes of scratch `workspace` that ssm_bwd needs (partial sums for dB, dC,
+ * dA, dD).  Returns 0 for an invalid desc. */
+size_t ssm_bwd_workspace_bytes(const ssm_desc_t* desc);
+
+/*
+ * Forward selective scan.
+ * Replaces: ssm_chunked_scan (selectssm.py:37-109), ssm_recursive_scan
+ * (ssmrecscan.py:36-77) and the custom-VJP forward ssm_scan_forward
+ * (ssmrecscan.py:85-88), plus the scan-adjacent epilogue of
+ * SelectiveSSM.__call__ (selectssm.py:230-238) and the gate of
+ * BidirectionalMamba (selectssm.py:335-336) when the flags ask for them.
+ *   y[b,p,q] = (scan(u,delta,A,Bc,Cc)[b,t,d] + skip) * gate
+ * with (p,q) = (t,d) or the reverse / complement map.
+ * Dskip is required iff SSM_SKIP, z iff SSM_GATE.  ckpt (ssm_ckpt_bytes) may
+ * be NULL for inference; ssm_bwd needs it.
+ */
+int ssm_fwd(void* stream, const ssm_desc_t* desc,
+            const void* u, const void* delta, const float* A,
+            const void* Bc, const void* Cc, const float* Dskip, const void* z,
+            void* y, float* ckpt);
+
+/*
+ * Backward of ssm_fwd for upstream gradient dy (same layout as y).
+ * Replaces the custom-VJP backward ssm_scan_backward / _recursive
+ * (ssmrecscan.py:111-181); with flags, also the autodiff of the epilogue
+ * (selectssm.py:230-238, 335-336).
+ * Outputs du, ddelta (B,L,D or B,L,1), dA (D,N), dB, dC (B,L,N); dD (D,)
+ * iff SSM_SKIP; dz iff SSM_GATE.  ckpt is the buffer ssm_fwd filled with the
+ * same inputs; workspace has ssm_bwd_workspace_bytes.  Deterministic.
+ */
+int ssm_bwd(void* stream, const ssm_desc_t* desc,
+            const void* u, const void* delta, const float* A,
+            const void* Bc, const void* Cc, const float* Dskip, const void* z,
+            const float* ckpt, const void* dy,
+            void* du, void* ddelta, float* dA, void* dB, void* dC,
+            float* dD, void* dz, void* workspace);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SELECTSSM_H */

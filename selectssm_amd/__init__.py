@@ -1,0 +1,26 @@
+"""selectssm_amd — MI355X (gfx950) selective scan behind the selectssm API.
+
+The hot path of ``selectssm`` (the selective scan y = scan(u, dt, A, B, C) with
+its custom-VJP backward, plus the scan-adjacent epilogue of ``SelectiveSSM`` /
+``BidirectionalMamba``) runs as hand-written HIP kernels exported through the C
+ABI in ``include/selectssm.h``.  There is no CPU fallback.
+"""
+from .scan import (
+    SelectiveScanFn,
+    largest_factor_up_to,
+    resolve_chunking,
+    selective_scan,
+    ssm_chunked_scan,
+    ssm_recursive_scan,
+    ssm_scan,
+)
+
+__all__ = [
+    "SelectiveScanFn",
+    "largest_factor_up_to",
+    "resolve_chunking",
+    "selective_scan",
+    "ssm_chunked_scan",
+    "ssm_recursive_scan",
+    "ssm_scan",
+]

@@ -1,0 +1,107 @@
+"""ctypes binding of the C ABI declared in ``include/selectssm.h``.
+
+The shared library is built in-tree (``selectssm_amd/libselectssm.so``).  There
+is no fallback: if the library is missing or fails to load, every op raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+from .build import LIB
+
+SSM_OK = 0
+SSM_ERR_INVALID = 1
+SSM_ERR_UNSUPPORTED = 2
+SSM_ERR_HIP = 3
+
+SSM_F32 = 0
+SSM_BF16 = 1
+
+SSM_REVERSE = 1
+SSM_COMPLEMENT = 2
+SSM_SKIP = 4
+SSM_GATE = 8
+
+ABI_VERSION = 1
+
+# every symbol include/selectssm.h declares
+EXPORTS = (
+    "ssm_abi_version",
+    "ssm_last_error",
+    "ssm_ckpt_bytes",
+    "ssm_bwd_workspace_bytes",
+    "ssm_fwd",
+    "ssm_bwd",
+)
+
+
+class SsmDesc(ctypes.Structure):
+    """Mirror of ``ssm_desc_t``."""
+
+    _fields_ = [
+        ("batch", ctypes.c_int64),
+        ("seqlen", ctypes.c_int64),
+        ("dim", ctypes.c_int64),
+        ("dstate", ctypes.c_int64),
+        ("dtype", ctypes.c_int32),
+        ("flags", ctypes.c_uint32),
+        ("delta_broadcast", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+class SsmError(RuntimeError):
+    """A nonzero return code from the library, with its ssm_last_error() text."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"selectssm error {code}: {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def _declare(lib):
+    vp = ctypes.c_void_p
+    fp = ctypes.c_void_p
+    dp = ctypes.POINTER(SsmDesc)
+    lib.ssm_abi_version.restype = ctypes.c_int
+    lib.ssm_abi_version.argtypes = []
+    lib.ssm_last_error.restype = ctypes.c_char_p
+    lib.ssm_last_error.argtypes = []
+    lib.ssm_ckpt_bytes.restype = ctypes.c_size_t
+    lib.ssm_ckpt_bytes.argtypes = [dp]
+    lib.ssm_bwd_workspace_bytes.restype = ctypes.c_size_t
+    lib.ssm_bwd_workspace_bytes.argtypes = [dp]
+    lib.ssm_fwd.restype = ctypes.c_int
+    lib.ssm_fwd.argtypes = [vp, dp, vp, vp, fp, vp, vp, fp, vp, vp, fp]
+    lib.ssm_bwd.restype = ctypes.c_int
+    lib.ssm_bwd.argtypes = [vp, dp, vp, vp, fp, vp, vp, fp, vp, fp, vp, vp, vp, fp, vp, vp, fp, vp, vp]
+
+
+def lib():
+    """The loaded library (loaded on first use).  Raises if it cannot load."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB):
+            raise RuntimeError(
+                f"{LIB} is missing: build it with `python -m selectssm_amd.build` "
+                "(there is no CPU fallback for the selective scan)")
+        handle = ctypes.CDLL(LIB)
+        _declare(handle)
+        got = handle.ssm_abi_version()
+        if got != ABI_VERSION:
+            raise RuntimeError(f"{LIB} has ABI version {got}, expected {ABI_VERSION}")
+        _lib = handle
+    return _lib
+
+
+def check(code: int) -> None:
+    if code != SSM_OK:
+        raise SsmError(code, lib().ssm_last_error().decode())
+
+
+def make_desc(batch, seqlen, dim, dstate, dtype=SSM_F32, flags=0, delta_broadcast=False) -> SsmDesc:
+    return SsmDesc(int(batch), int(seqlen), int(dim), int(dstate), int(dtype), int(flags),
+                   1 if delta_broadcast else 0, 0)

@@ -1,0 +1,243 @@
+"""Host side of the selective scan: torch tensors in, HIP kernels through the C ABI.
+
+Public functions keep the reference's names, argument order and errors:
+
+* ``ssm_chunked_scan``   — selectssm.py:37-109
+* ``ssm_recursive_scan`` — ssmrecscan.py:36-77
+* ``ssm_scan``           — ssmrecscan.py:80-88, 163-183 (custom VJP)
+
+All three run the same fused kernel pair (``ssm_fwd`` / ``ssm_bwd``) and are
+differentiable through :class:`SelectiveScanFn`, whose backward is the custom
+VJP's adjoint.  The reference's chunking / recursion arguments are validated
+exactly as the reference does and otherwise do not change the result (the
+reference's strategies agree up to fp32 rounding; the kernel's blocking is
+internal).
+
+:func:`selective_scan` is the fused op with the scan-adjacent epilogue of
+``SelectiveSSM`` / ``BidirectionalMamba``: D-skip (selectssm.py:238), silu(z)
+gate (selectssm.py:335-336) and the reverse / complement index maps
+(selectssm.py:167-168, 230-231).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _lib as L
+
+
+# ---------------------------------------------------------------- host logic
+
+def largest_factor_up_to(b: int, n: int) -> int:
+    """Largest divisor of ``n`` not above ``b``; ``n`` itself when n < 2 (selectssm.py:24-30)."""
+    if n < 2:
+        return n
+    k = b
+    while n % k != 0:
+        k -= 1
+    return k
+
+
+def resolve_chunking(L_: int, D: int, chunk_size=None, n_channel_groups=1):
+    """``(chunk_size, K)`` with the reference's defaults and ValueErrors (selectssm.py:43-55)."""
+    K = n_channel_groups if n_channel_groups is not None else 1
+    if D % K != 0:
+        raise ValueError(f"n_channel_groups={n_channel_groups} must divide D={D}")
+    if chunk_size is None:
+        chunk_size = largest_factor_up_to(int(math.sqrt(K * L_)), L_)
+    if L_ % chunk_size != 0:
+        raise ValueError(f"chunk_size={chunk_size} must divide L={L_}")
+    return chunk_size, K
+
+
+_IO_DTYPES = {torch.float32: L.SSM_F32, torch.bfloat16: L.SSM_BF16}
+
+
+def _io_dtype(*ts):
+    dt = None
+    for t in ts:
+        if t is None:
+            continue
+        dt = t.dtype if dt is None else torch.promote_types(dt, t.dtype)
+    if dt not in _IO_DTYPES:
+        raise TypeError(f"selective scan supports float32 and bfloat16 activations, got {dt}")
+    return dt
+
+
+def _check_shapes(u, delta, A, B, C, Dskip, z):
+    if u.dim() != 3:
+        raise ValueError(f"x must be (B, L, D), got shape {tuple(u.shape)}")
+    Bt, Ln, D = u.shape
+    if A.dim() != 2 or A.shape[0] != D:
+        raise ValueError(f"Acoeff must be (D, N) with D={D}, got {tuple(A.shape)}")
+    N = A.shape[1]
+    for name, t in (("Bcoeff", B), ("Ccoeff", C)):
+        if tuple(t.shape) != (Bt, Ln, N):
+            raise ValueError(f"{name} must be (B, L, N)=({Bt}, {Ln}, {N}), got {tuple(t.shape)}")
+    if tuple(delta.shape) not in ((Bt, Ln, D), (Bt, Ln, 1)):
+        raise ValueError(f"dt must be (B, L, D) or (B, L, 1), got {tuple(delta.shape)}")
+    if Dskip is not None and tuple(Dskip.shape) != (D,):
+        raise ValueError(f"D must be ({D},), got {tuple(Dskip.shape)}")
+    if z is not None and tuple(z.shape) != (Bt, Ln, D):
+        raise ValueError(f"z must be (B, L, D), got {tuple(z.shape)}")
+    for t in (u, delta, A, B, C, Dskip, z):
+        if t is not None and not t.is_cuda:
+            raise ValueError("selective scan inputs must be GPU tensors (there is no CPU path)")
+    return Bt, Ln, D, N
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _flags(skip, gate, reverse, complement):
+    f = 0
+    if reverse:
+        f |= L.SSM_REVERSE
+        if complement:
+            f |= L.SSM_COMPLEMENT
+    if skip:
+        f |= L.SSM_SKIP
+    if gate:
+        f |= L.SSM_GATE
+    return f
+
+
+def _desc(u, delta, A, flags):
+    Bt, Ln, D = u.shape
+    return L.make_desc(Bt, Ln, D, A.shape[1], _IO_DTYPES[u.dtype], flags,
+                       delta_broadcast=(delta.shape[-1] == 1 and D != 1))
+
+
+# ------------------------------------------------------------- raw launchers
+
+def scan_fwd(u, delta, A, B, C, Dskip=None, z=None, reverse=False, complement=False, want_ckpt=True):
+    """Run ``ssm_fwd``.  All tensors contiguous, on one GPU, I/O dtype shared.
+
+    Returns ``(y, ckpt)``; ``ckpt`` is None when ``want_ckpt`` is False.
+    """
+    flags = _flags(Dskip is not None, z is not None, reverse, complement)
+    desc = _desc(u, delta, A, flags)
+    lib = L.lib()
+    y = torch.empty_like(u)
+    ckpt = None
+    if want_ckpt:
+        nbytes = lib.ssm_ckpt_bytes(ctypes.byref(desc))
+        if nbytes == 0:
+            L.check(L.SSM_ERR_INVALID)
+        ckpt = torch.empty(nbytes // 4, dtype=torch.float32, device=u.device)
+    L.check(lib.ssm_fwd(_stream(), ctypes.byref(desc), _ptr(u), _ptr(delta), _ptr(A), _ptr(B), _ptr(C),
+                        _ptr(Dskip), _ptr(z), _ptr(y), _ptr(ckpt)))
+    return y, ckpt
+
+
+def scan_bwd(u, delta, A, B, C, Dskip, z, ckpt, dy, reverse=False, complement=False):
+    """Run ``ssm_bwd``.  Returns ``(du, ddelta, dA, dB, dC, dD, dz)`` (dD / dz None when unused)."""
+    flags = _flags(Dskip is not None, z is not None, reverse, complement)
+    desc = _desc(u, delta, A, flags)
+    lib = L.lib()
+    du = torch.empty_like(u)
+    ddelta = torch.empty_like(delta)
+    dA = torch.empty_like(A)
+    dB = torch.empty_like(B)
+    dC = torch.empty_like(C)
+    dD = torch.empty_like(Dskip) if Dskip is not None else None
+    dz = torch.empty_like(z) if z is not None else None
+    nbytes = lib.ssm_bwd_workspace_bytes(ctypes.byref(desc))
+    if nbytes == 0:
+        L.check(L.SSM_ERR_INVALID)
+    ws = torch.empty(nbytes // 4, dtype=torch.float32, device=u.device)
+    L.check(lib.ssm_bwd(_stream(), ctypes.byref(desc), _ptr(u), _ptr(delta), _ptr(A), _ptr(B), _ptr(C),
+                        _ptr(Dskip), _ptr(z), _ptr(ckpt), _ptr(dy), _ptr(du), _ptr(ddelta), _ptr(dA),
+                        _ptr(dB), _ptr(dC), _ptr(dD), _ptr(dz), _ptr(ws)))
+    return du, ddelta, dA, dB, dC, dD, dz
+
+
+# ------------------------------------------------------------------- autograd
+
+class SelectiveScanFn(torch.autograd.Function):
+    """y = epilogue(scan(u, delta, A, B, C)) with the custom-VJP backward.
+
+    The saved residuals are the inputs plus the forward's state checkpoints
+    (the reference saves only the inputs, ssmrecscan.py:88, and recomputes
+    recursively in the backward, ssmrecscan.py:111-161).
+    """
+
+    @staticmethod
+    def forward(ctx, u, delta, A, B, C, Dskip, z, reverse, complement):
+        y, ckpt = scan_fwd(u, delta, A, B, C, Dskip, z, reverse, complement,
+                           want_ckpt=torch.is_grad_enabled() or any(ctx.needs_input_grad))
+        ctx.save_for_backward(u, delta, A, B, C, Dskip, z, ckpt)
+        ctx.flags = (reverse, complement)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        u, delta, A, B, C, Dskip, z, ckpt = ctx.saved_tensors
+        dy = dy.to(u.dtype).contiguous()
+        du, ddelta, dA, dB, dC, dD, dz = scan_bwd(u, delta, A, B, C, Dskip, z, ckpt, dy, *ctx.flags)
+        return du, ddelta, dA, dB, dC, dD, dz, None, None
+
+
+def selective_scan(u, delta, A, B, C, D=None, z=None, reverse=False, complement=False):
+    """Fused selective scan with the SelectiveSSM / BidirectionalMamba epilogue.
+
+    u, delta, B, C are in the scan domain (flipped already when ``reverse``,
+    as SelectiveSSM builds them from the flipped x, selectssm.py:167-210);
+    the output is in the original domain:
+        y = scan(u, delta, A, B, C)              (selectssm.py:222-228)
+        y = flip(y)            if reverse        (selectssm.py:230-231)
+        y = y + u * D          if D is given     (selectssm.py:238; u stays flipped)
+        y = y * silu(z)        if z is given     (selectssm.py:335-336)
+    ``complement`` (with ``reverse``) also mirrors the channel axis.
+    """
+    Bt, Ln, Dm, N = _check_shapes(u, delta, A, B, C, D, z)
+    if complement and not reverse:
+        complement = False  # the reference only looks at complement when reverse (selectssm.py:116)
+    io = _io_dtype(u, delta, B, C, z)
+    cast = lambda t: None if t is None else t.to(io).contiguous()
+    fcast = lambda t: None if t is None else t.to(torch.float32).contiguous()
+    return SelectiveScanFn.apply(cast(u), cast(delta), fcast(A), cast(B), cast(C), fcast(D), cast(z),
+                                 bool(reverse), bool(complement))
+
+
+# ------------------------------------------------------- reference-named API
+
+def ssm_chunked_scan(x, Acoeff, Bcoeff, Ccoeff, dt, chunk_size: int = None, n_channel_groups: int = 1):
+    """Drop-in for ``ssm_chunked_scan`` (selectssm.py:37-109).
+
+    Same arguments and ValueErrors (selectssm.py:47-48, 53-54); the result does
+    not depend on ``chunk_size`` / ``n_channel_groups`` beyond fp32 rounding.
+    """
+    if x.dim() != 3:
+        raise ValueError(f"x must be (B, L, D), got shape {tuple(x.shape)}")
+    resolve_chunking(x.shape[-2], x.shape[-1], chunk_size, n_channel_groups)
+    return selective_scan(x, dt, Acoeff, Bcoeff, Ccoeff)
+
+
+def _check_recursion(min_recursion_length, recursive_split):
+    if recursive_split < 2:
+        # the reference recurses without end for split 1 (ssmrecscan.py:56-63)
+        raise RecursionError(f"recursive_split={recursive_split} never shortens the sequence")
+
+
+def ssm_recursive_scan(x, Acoeff, Bcoeff, Ccoeff, Delta, min_recursion_length: int = 2, recursive_split: int = 2):
+    """Drop-in for ``ssm_recursive_scan`` (ssmrecscan.py:36-77)."""
+    _check_recursion(min_recursion_length, recursive_split)
+    return selective_scan(x, Delta, Acoeff, Bcoeff, Ccoeff)
+
+
+def ssm_scan(x, Acoeff, Bcoeff, Ccoeff, Delta, min_recursion_length: int = 2, recursive_split: int = 2):
+    """Drop-in for the custom-VJP ``ssm_scan`` (ssmrecscan.py:80-88, 163-183).
+
+    Its gradient is the custom VJP's adjoint (du, dA, dB, dC, ddelta), computed
+    by ``ssm_bwd`` from the inputs and the forward's checkpoints.
+    """
+    _check_recursion(min_recursion_length, recursive_split)
+    return selective_scan(x, Delta, Acoeff, Bcoeff, Ccoeff)
