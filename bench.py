@@ -1,0 +1,169 @@
+#!/usr/bin/env python
+"""Selective-scan fwd+bwd throughput on one MI355X (BASELINE.json metric).
+
+Workload: the custom-VJP selective scan of a
+SelectiveSSM block, B=8, L=8192, D_inner=2048, N=16, fp32, loss = sum(y * g).
+One step = ssm_fwd (with the checkpoints the backward needs) + ssm_bwd over one
+batch of synthetic inputs already resident in HBM.  value = B*L*steps / time.
+
+The JSON line also carries
+  roofline      for the dominant launch (ssm_bwd): algorithmic bytes per launch
+                / its mean duration from HIP events on the launch stream,
+                against MI355X's 8 TB/s; `traffic` = HBM bytes per launch from
+                rocprofv3 FETCH_SIZE/WRITE_SIZE (profiles/traffic_c1.txt), or null
+  cpu_baseline  the CPU restatement of the reference's custom-VJP path
+                (oracle/ssm_oracle.c), timed on this host's cores on a sample
+                of the same workload
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+HBM_PEAK_GBS = 8000.0
+CONFIG = dict(batch=8, seqlen=8192, dim=2048, dstate=16)
+
+
+def alg_bytes(B, L, D, N, w=4):
+    """Compulsory op-boundary bytes: every input read once, every output written once."""
+    fwd = (3 * B * L * D + 2 * B * L * N) * w + 4 * D * N            # u, dt, y; B, C; A
+    bwd = (5 * B * L * D + 4 * B * L * N) * w + 8 * D * N            # u, dt, dy, du, ddt; B, C, dB, dC; A, dA
+    return fwd, bwd
+
+
+def read_traffic(path):
+    """HBM bytes per ssm_bwd launch from a rocprofv3 PMC summary, or None."""
+    if not os.path.exists(path):
+        return None
+    vals = {}
+    with open(path) as f:
+        for line in f:
+            if ":" in line and not line.startswith("#"):
+                k, v = line.split(":", 1)
+                vals[k.strip()] = v.strip()
+    try:
+        return float(vals["traffic_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
+
+
+def cpu_baseline(B, L, D, N):
+    """Time the C port of the reference's custom-VJP path on a sample: one batch row."""
+    import numpy as np
+    from oracle import c_oracle
+    from selectssm_amd.synthetic import make_inputs
+
+    cores = len(os.sched_getaffinity(0))
+    sb = 1
+    inp = make_inputs(sb, L, D, N, seed=0)
+    args = (inp["u"], inp["dt"], inp["A"], inp["B"], inp["C"])
+    times = []
+    for rep in range(3):  # first run is the warmup
+        t0 = time.perf_counter()
+        c_oracle.scan_fwd(*args, nthreads=cores)
+        c_oracle.scan_bwd(*args, inp["g"], nthreads=cores)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times[1:]))
+    return {
+        "value": sb * L / t,
+        "unit": "tokens/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"fwd+bwd of batch rows 1 of {B} (L={L}, D={D}, N={N}, fp32), recursive custom-VJP "
+                  f"algorithm (min_recursion_length=2, recursive_split=2), median of 2 after 1 warmup, "
+                  f"{t:.2f} s per run",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the scan's multi-GPU "
+              "sharding is a design note, not a measured path", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from selectssm_amd.scan import scan_bwd, scan_fwd
+    from selectssm_amd.synthetic import make_inputs_gpu
+
+    B, L, D, N = CONFIG["batch"], CONFIG["seqlen"], CONFIG["dim"], CONFIG["dstate"]
+    x = make_inputs_gpu(B, L, D, N, seed=0)
+    u, dt, A, Bc, Cc, g = x["u"], x["dt"], x["A"], x["B"], x["C"], x["g"]
+
+    def step():
+        y, ckpt = scan_fwd(u, dt, A, Bc, Cc)
+        return scan_bwd(u, dt, A, Bc, Cc, None, None, ckpt, g)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    K = args.steps
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(K)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(K):
+        ev[k][0].record()
+        y, ckpt = scan_fwd(u, dt, A, Bc, Cc)
+        ev[k][1].record()
+        scan_bwd(u, dt, A, Bc, Cc, None, None, ckpt, g)
+        ev[k][2].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / K
+    bwd_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / K
+    fwd_b, bwd_b = alg_bytes(B, L, D, N)
+    tokens = B * L * K
+    achieved = bwd_b / (bwd_ms * 1e-3) / 1e9
+    traffic = read_traffic(os.path.join(REPO, "profiles", "traffic_c1.txt"))
+
+    line = {
+        "metric": "selective-scan fwd+bwd tokens/s and % of HBM roofline on 1 MI355X",
+        "value": tokens / wall,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": wall * 1e3 / K,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (BASELINE.json configs[1] distributions, torch generator, seed 0)",
+        "config": {"workload": "SelectiveSSM custom_vjp_scan selective scan fwd+bwd (configs[1])",
+                   "batch": B, "seqlen": L, "d_inner": D, "d_state": N, "io": "f32"},
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "ssm_bwd (ssm_bwd_kernel + partial-sum reductions)",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": traffic,
+            "alg_bytes_per_launch": bwd_b,
+            "mean_launch_ms": bwd_ms,
+        },
+        "step_roofline_frac": (fwd_b + bwd_b) / (wall / K) / 1e9 / HBM_PEAK_GBS,
+        "fwd": {"mean_launch_ms": fwd_ms, "alg_bytes_per_launch": fwd_b,
+                "achieved_GBs": fwd_b / (fwd_ms * 1e-3) / 1e9},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(B, L, D, N)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -34,9 +34,13 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kWave = 64;
-constexpr int kNPW = 4;   // states per wave
-constexpr int kCK = 16;   // checkpoint interval = backward block length
-constexpr int kTB = 16;   // forward staging block for the cross-wave y sum
+// checkpoint interval = backward block length (8 only where 16 would not fit in LDS)
+__host__ __device__ constexpr int ck_for(int ng, bool epi) { return (ng >= 8 && epi) ? 8 : 16; }
+#ifndef SSM_PLAIN_NPW
+#define SSM_PLAIN_NPW 2
+#endif
+constexpr int kPlainNPW = SSM_PLAIN_NPW;  // states per wave of the plain scan
+constexpr int kTT = 32;   // forward time tile staged in LDS (a multiple of kCK)
 
 // ---------------------------------------------------------------- element I/O
 
@@ -108,7 +112,14 @@ __device__ __forceinline__ float wave_reduce4(float x0, float x1, float x2, floa
   float q = __uint_as_float(s[0]) + __uint_as_float(s[1]);  // row0 x0, row1 x2, row2 x1, row3 x3
   return row_sum16(q);
 }
-__device__ constexpr int kRowState[4] = {0, 2, 1, 3};
+
+// Two per-lane values over all 64 lanes: rows 0,1 hold the total of x0, rows 2,3 of x1.
+__device__ __forceinline__ float wave_reduce2(float x0, float x1) {
+  auto s01 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x0), __float_as_uint(x1), false, false);
+  const float p = __uint_as_float(s01[0]) + __uint_as_float(s01[1]);  // lanes < 32: x0; >= 32: x1
+  auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(p), __float_as_uint(p), false, false);
+  return row_sum16(__uint_as_float(s[0]) + __uint_as_float(s[1]));
+}
 
 // Full sum of one value over the wave (every lane gets it).
 __device__ __forceinline__ float wave_sum(float v) {
@@ -116,6 +127,53 @@ __device__ __forceinline__ float wave_sum(float v) {
   v += __shfl_xor(v, 16);
   v += __shfl_xor(v, 32);
   return v;
+}
+
+// Sum over the wave of each of the NPW per-lane values.  The totals land in a
+// few lanes; wave_reduce_state(lane) names the value a lane holds (-1: none).
+template <int NPW>
+__device__ __forceinline__ float wave_reduce(const float (&x)[NPW]) {
+  if constexpr (NPW == 4) return wave_reduce4(x[0], x[1], x[2], x[3]);
+  else if constexpr (NPW == 2) return wave_reduce2(x[0], x[1]);
+  else return wave_sum(x[0]);
+}
+template <int NPW>
+__device__ __forceinline__ int wave_reduce_state(int lane) {
+  if constexpr (NPW == 4) return (lane & 15) == 0 ? (0x3120 >> (4 * (lane >> 4))) & 0xf : -1;  // rows hold x0,x2,x1,x3
+  else if constexpr (NPW == 2) return (lane & 31) == 0 ? lane >> 5 : -1;
+  else return lane == 0 ? 0 : -1;
+}
+
+// NPW consecutive floats from (16-byte aligned) LDS in one read
+template <int NPW>
+__device__ __forceinline__ void lds_vec(const float* p, float (&o)[NPW]) {
+  if constexpr (NPW == 4) {
+    const float4 v = *reinterpret_cast<const float4*>(p);
+    o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+  } else if constexpr (NPW == 2) {
+    const float2 v = *reinterpret_cast<const float2*>(p);
+    o[0] = v.x; o[1] = v.y;
+  } else {
+    o[0] = *p;
+  }
+}
+
+// ------------------------------------------------------------- staged tiles
+//
+// Each kernel walks time in tiles.  While a tile is being computed from LDS,
+// the next tile's inputs are already in flight into registers (fetch), and
+// are written to the other LDS buffer after the tile (commit).  Thread
+// (wave w, lane c) stages rows i = w, w+NG, ... of a [rows][64] tile, column c,
+// so every global access of a wave is one contiguous 64-element row.
+
+// element (scan step t, lane channel d) of a (B,L,D) array, optionally read at
+// the mirrored output position (L-1-t, D-1-d); 0 outside the tensor
+template <typename T>
+__device__ __forceinline__ float ld_at(const T* X, int64_t bLD, int L, int D, int t, int d, bool rev, bool comp) {
+  if (t >= L || d >= D) return 0.0f;
+  const int r = rev ? L - 1 - t : t;
+  const int c = comp ? D - 1 - d : d;
+  return ld(X, bLD + (int64_t)r * D + c);
 }
 
 // ------------------------------------------------------------------ forward
@@ -136,8 +194,16 @@ struct FwdArgs {
   uint32_t flags;
 };
 
-template <int NG, typename T>
+// NPW states per wave, NG waves per workgroup (NPW*NG >= N), EPI: the skip /
+// gate epilogue is fused (its extra staging only exists in EPI builds).
+template <int NPW, int NG, bool EPI, typename T>
 __global__ void __launch_bounds__(kWave* NG, 1) ssm_fwd_kernel(FwdArgs<T> p) {
+  constexpr int kCK = ck_for(NG, EPI);
+  static_assert(kTT % kCK == 0, "time tile must hold whole checkpoint blocks");
+  constexpr int NS = NG * NPW;                                     // padded state count
+  constexpr int RPT = kTT / NG;                                    // staged rows per thread
+  constexpr int BCE = (kTT * NS + kWave * NG - 1) / (kWave * NG);  // staged B/C elements per thread
+  constexpr int EB = EPI ? 2 : 1;                                  // epilogue staging buffers
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int b = blockIdx.y;
@@ -145,72 +211,141 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_fwd_kernel(FwdArgs<T> p) {
   const int d = blockIdx.x * kWave + lane;
   const bool valid = d < D;
   const int dc = valid ? d : 0;
-  const int n0 = wave * kNPW;
+  const int n0 = wave * NPW;
+  const bool rev = p.flags & SSM_REVERSE;
+  const bool comp = rev && (p.flags & SSM_COMPLEMENT);
+  const bool skip = EPI && (p.flags & SSM_SKIP);
+  const bool gate = EPI && (p.flags & SSM_GATE);
+  const bool stage_eu = skip && rev;  // u at the output position is another element
+  const int q = comp ? D - 1 - dc : dc;
+  const float Dq = (skip && valid) ? p.Dskip[q] : 0.0f;
 
-  float A2[kNPW], h[kNPW];
+  float A2[NPW], h[NPW];
 #pragma unroll
-  for (int j = 0; j < kNPW; ++j) {
+  for (int j = 0; j < NPW; ++j) {
     const int n = n0 + j;
     A2[j] = (valid && n < N) ? p.A[(int64_t)dc * N + n] * kLog2e : 0.0f;
     h[j] = 0.0f;
   }
 
-  __shared__ float ybuf[NG][kTB][kWave];
+  __shared__ float s_u[2][kTT][kWave], s_dt[2][kTT][kWave];
+  __shared__ float s_eu[EB][EPI ? kTT : 1][kWave], s_ez[EB][EPI ? kTT : 1][kWave];
+  __shared__ __attribute__((aligned(16))) float s_B[2][kTT][NS];
+  __shared__ __attribute__((aligned(16))) float s_C[2][kTT][NS];
+  __shared__ float s_y[NG][kTT][kWave];
 
-  const int64_t rowD = (int64_t)b * L * D;  // (b,0,0) in (B,L,D)
-  const int64_t rowN = (int64_t)b * L * N;  // (b,0,0) in (B,L,N)
-  const int64_t rowDt = (int64_t)b * L * (p.dstride ? D : 1);
+  const int64_t bLD = (int64_t)b * L * D;
+  const int64_t bLN = (int64_t)b * L * N;
   const int dtD = p.dstride ? D : 1;
+  const int64_t bLDt = (int64_t)b * L * dtD;
   const int dd_lane = p.dstride ? dc : 0;
-  const bool rev = p.flags & SSM_REVERSE;
-  const bool comp = rev && (p.flags & SSM_COMPLEMENT);
 
-  for (int t0 = 0; t0 < L; t0 += kTB) {
-    const int tn = min(kTB, L - t0);
-#pragma unroll 4
-    for (int i = 0; i < tn; ++i) {
-      const int t = t0 + i;
-      if (p.ckpt != nullptr && (t % kCK) == 0) {
-        const int blk = t / kCK;
+  float r_u[RPT], r_dt[RPT], r_eu[RPT], r_ez[RPT], r_B[BCE], r_C[BCE];
+  auto fetch = [&](int t0) {
 #pragma unroll
-        for (int j = 0; j < kNPW; ++j) {
-          const int n = n0 + j;
-          if (valid && n < N) p.ckpt[(((int64_t)b * p.nblk + blk) * N + n) * D + d] = h[j];
+    for (int k = 0; k < RPT; ++k) {
+      const int t = t0 + wave + k * NG;
+      const bool in = valid && t < L;
+      r_u[k] = in ? ld(p.u, bLD + (int64_t)t * D + dc) : 0.0f;
+      r_dt[k] = in ? ld(p.delta, bLDt + (int64_t)t * dtD + dd_lane) : 0.0f;
+      if (stage_eu) r_eu[k] = ld_at(p.u, bLD, L, D, t, d, rev, comp);
+      if (gate) r_ez[k] = ld_at(p.z, bLD, L, D, t, d, rev, comp);
+    }
+#pragma unroll
+    for (int k = 0; k < BCE; ++k) {
+      const int e = threadIdx.x + k * kWave * NG;
+      const int i = e / NS, n = e - (e / NS) * NS;
+      const bool in = e < kTT * NS && t0 + i < L && n < N;
+      r_B[k] = in ? ld(p.Bc, bLN + (int64_t)(t0 + i) * N + n) : 0.0f;
+      r_C[k] = in ? ld(p.Cc, bLN + (int64_t)(t0 + i) * N + n) : 0.0f;
+    }
+  };
+  auto commit = [&](int buf) {
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      const int i = wave + k * NG;
+      s_u[buf][i][lane] = r_u[k];
+      s_dt[buf][i][lane] = r_dt[k];
+      if (stage_eu) s_eu[buf][i][lane] = r_eu[k];
+      if (gate) s_ez[buf][i][lane] = r_ez[k];
+    }
+#pragma unroll
+    for (int k = 0; k < BCE; ++k) {
+      const int e = threadIdx.x + k * kWave * NG;
+      if (e < kTT * NS) {
+        const int i = e / NS, n = e - (e / NS) * NS;
+        s_B[buf][i][n] = r_B[k];
+        s_C[buf][i][n] = r_C[k];
+      }
+    }
+  };
+
+  fetch(0);
+  commit(0);
+  __syncthreads();
+  int buf = 0;
+  for (int t0 = 0; t0 < L; t0 += kTT, buf ^= 1) {
+    const bool more = t0 + kTT < L;
+    if (more) fetch(t0 + kTT);
+    const int tn = min(kTT, L - t0);
+    auto tile = [&](auto full_tag) {
+      constexpr bool kFull = decltype(full_tag)::value;
+      // operands of the whole tile in registers first, so no step waits on LDS
+      float uu[kTT], dd[kTT], ys[kTT];
+#pragma unroll
+      for (int i = 0; i < kTT; ++i) {
+        if (kFull || i < tn) {
+          uu[i] = s_u[buf][i][lane];
+          dd[i] = s_dt[buf][i][lane];
         }
       }
-      const float uu = valid ? ld(p.u, rowD + (int64_t)t * D + dc) : 0.0f;
-      const float dd = valid ? ld(p.delta, rowDt + (int64_t)t * dtD + dd_lane) : 0.0f;
-      const float w = dd * uu;
-      float yp = 0.0f;
 #pragma unroll
-      for (int j = 0; j < kNPW; ++j) {
-        const int n = n0 + j;
-        const float Bn = n < N ? ld(p.Bc, rowN + (int64_t)t * N + n) : 0.0f;
-        const float Cn = n < N ? ld(p.Cc, rowN + (int64_t)t * N + n) : 0.0f;
-        const float a = fast_exp2(A2[j] * dd);
-        h[j] = fmaf(a, h[j], Bn * w);
-        yp = fmaf(Cn, h[j], yp);
+      for (int i = 0; i < kTT; ++i) {
+        if (kFull || i < tn) {
+          float Bn[NPW], Cn[NPW];
+          lds_vec<NPW>(&s_B[buf][i][n0], Bn);
+          lds_vec<NPW>(&s_C[buf][i][n0], Cn);
+          if (p.ckpt != nullptr && (i % kCK) == 0) {
+            const int blk = (t0 + i) / kCK;
+#pragma unroll
+            for (int j = 0; j < NPW; ++j) {
+              const int n = n0 + j;
+              if (valid && n < N) p.ckpt[(((int64_t)b * p.nblk + blk) * N + n) * D + d] = h[j];
+            }
+          }
+          const float w = dd[i] * uu[i];
+          float yp = 0.0f;
+#pragma unroll
+          for (int j = 0; j < NPW; ++j) {
+            const float a = fast_exp2(A2[j] * dd[i]);
+            h[j] = fmaf(a, h[j], Bn[j] * w);
+            yp = fmaf(Cn[j], h[j], yp);
+          }
+          ys[i] = yp;
+        }
       }
-      ybuf[wave][i][lane] = yp;
-    }
+#pragma unroll
+      for (int i = 0; i < kTT; ++i)
+        if (kFull || i < tn) s_y[wave][i][lane] = ys[i];
+    };
+    if (tn == kTT) tile(std::true_type{}); else tile(std::false_type{});
     __syncthreads();
     for (int i = wave; i < tn; i += NG) {
       float ys = 0.0f;
 #pragma unroll
-      for (int w = 0; w < NG; ++w) ys += ybuf[w][i][lane];
+      for (int w = 0; w < NG; ++w) ys += s_y[w][i][lane];
       if (valid) {
         const int t = t0 + i;
         const int pt = rev ? L - 1 - t : t;
-        const int q = comp ? D - 1 - d : d;
-        const int64_t o = rowD + (int64_t)pt * D + q;
-        if (p.flags & SSM_SKIP) ys += ld(p.u, o) * p.Dskip[q];
-        if (p.flags & SSM_GATE) {
-          const float zz = ld(p.z, o);
+        if (skip) ys = fmaf(stage_eu ? s_eu[buf][i][lane] : s_u[buf][i][lane], Dq, ys);
+        if (gate) {
+          const float zz = s_ez[buf][i][lane];
           ys *= zz * sigmoid(zz);
         }
-        st(p.y, o, ys);
+        st(p.y, bLD + (int64_t)pt * D + q, ys);
       }
     }
+    if (more) commit(buf ^ 1);
     __syncthreads();
   }
 }
@@ -241,18 +376,14 @@ struct BwdArgs {
   uint32_t flags;
 };
 
-template <typename T>
-__device__ __forceinline__ float gated_dy(const BwdArgs<T>& p, int64_t o) {
-  float g = ld(p.dy, o);
-  if (p.flags & SSM_GATE) {
-    const float zz = ld(p.z, o);
-    g *= zz * sigmoid(zz);
-  }
-  return g;
-}
-
-template <int NG, typename T>
+template <int NPW, int NG, bool EPI, typename T>
 __global__ void __launch_bounds__(kWave* NG, 1) ssm_bwd_kernel(BwdArgs<T> p) {
+  constexpr int kCK = ck_for(NG, EPI);
+  constexpr int NS = NG * NPW;
+  constexpr int RPT = kCK / NG;
+  constexpr int BCE = (kCK * NS + kWave * NG - 1) / (kWave * NG);
+  constexpr int EB = EPI ? 2 : 1;
+  constexpr int ER = EPI ? kCK : 1;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int b = blockIdx.y;
@@ -261,16 +392,20 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_bwd_kernel(BwdArgs<T> p) {
   const int d = cb * kWave + lane;
   const bool valid = d < D;
   const int dc = valid ? d : 0;
-  const int n0 = wave * kNPW;
+  const int n0 = wave * NPW;
   const bool rev = p.flags & SSM_REVERSE;
   const bool comp = rev && (p.flags & SSM_COMPLEMENT);
-  const bool gate = p.flags & SSM_GATE;
-  const bool skip = p.flags & SSM_SKIP;
-  const int q = comp ? D - 1 - dc : dc;  // output channel of this lane
+  const bool gate = EPI && (p.flags & SSM_GATE);
+  const bool skip = EPI && (p.flags & SSM_SKIP);
+  const bool stage_dyo = skip && rev;         // gated dy at the unmirrored (t,d) for the skip term
+  const bool stage_eu = gate && skip && rev;  // u at the output position for y_pre
+  const int q = comp ? D - 1 - dc : dc;
+  const float Dd = (skip && valid) ? p.Dskip[dc] : 0.0f;
+  const float Dq = (skip && valid) ? p.Dskip[q] : 0.0f;
 
-  float Av[kNPW], A2[kNPW], g[kNPW], dAacc[kNPW];
+  float Av[NPW], A2[NPW], g[NPW], dAacc[NPW];
 #pragma unroll
-  for (int j = 0; j < kNPW; ++j) {
+  for (int j = 0; j < NPW; ++j) {
     const int n = n0 + j;
     Av[j] = (valid && n < N) ? p.A[(int64_t)dc * N + n] : 0.0f;
     A2[j] = Av[j] * kLog2e;
@@ -279,96 +414,168 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_bwd_kernel(BwdArgs<T> p) {
   }
   float dDacc = 0.0f;
 
-  __shared__ float sbuf[3][NG][kCK][kWave];   // per-wave partials: du, ddelta, y
-  __shared__ float bcbuf[2][kCK][NG * kNPW];  // dB, dC wave partials
+  __shared__ float s_u[2][kCK][kWave], s_dt[2][kCK][kWave], s_dy[2][kCK][kWave];
+  __shared__ float s_go[EB][ER][kWave], s_gz[EB][ER][kWave];  // gate: raw dy and z at the output position
+  __shared__ float s_eu[EB][ER][kWave], s_dyo[EB][ER][kWave];
+  __shared__ __attribute__((aligned(16))) float s_B[2][kCK][NS];
+  __shared__ __attribute__((aligned(16))) float s_C[2][kCK][NS];
+  __shared__ float sbuf[EPI ? 3 : 2][NG][kCK][kWave];  // per-wave partials: du, ddelta, (y)
+  __shared__ float bcbuf[2][kCK][NS];                  // dB, dC wave partials
 
-  const int64_t rowD = (int64_t)b * L * D;
-  const int64_t rowN = (int64_t)b * L * N;
+  const int64_t bLD = (int64_t)b * L * D;
+  const int64_t bLN = (int64_t)b * L * N;
   const int dtD = p.dstride ? D : 1;
-  const int64_t rowDt = (int64_t)b * L * dtD;
+  const int64_t bLDt = (int64_t)b * L * dtD;
   const int dd_lane = p.dstride ? dc : 0;
 
-  for (int blk = p.nblk - 1; blk >= 0; --blk) {
+  float r_u[RPT], r_dt[RPT], r_dy[RPT], r_go[RPT], r_gz[RPT], r_eu[RPT], r_dyo[RPT];
+  float r_B[BCE], r_C[BCE], r_h[NPW];
+  auto fetch = [&](int blk) {
+    const int t0 = blk * kCK;
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      const int t = t0 + wave + k * NG;
+      const bool in = valid && t < L;
+      r_u[k] = in ? ld(p.u, bLD + (int64_t)t * D + dc) : 0.0f;
+      r_dt[k] = in ? ld(p.delta, bLDt + (int64_t)t * dtD + dd_lane) : 0.0f;
+      const float go = ld_at(p.dy, bLD, L, D, t, d, rev, comp);
+      if (gate) {
+        const float gz = ld_at(p.z, bLD, L, D, t, d, rev, comp);
+        r_go[k] = go;
+        r_gz[k] = gz;
+        r_dy[k] = go * gz * sigmoid(gz);
+      } else {
+        r_dy[k] = go;
+      }
+      if (stage_eu) r_eu[k] = ld_at(p.u, bLD, L, D, t, d, rev, comp);
+      if (stage_dyo) {
+        float v = ld_at(p.dy, bLD, L, D, t, d, false, false);
+        if (gate) {
+          const float zz = ld_at(p.z, bLD, L, D, t, d, false, false);
+          v *= zz * sigmoid(zz);
+        }
+        r_dyo[k] = v;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < BCE; ++k) {
+      const int e = threadIdx.x + k * kWave * NG;
+      const int i = e / NS, n = e - (e / NS) * NS;
+      const bool in = e < kCK * NS && t0 + i < L && n < N;
+      r_B[k] = in ? ld(p.Bc, bLN + (int64_t)(t0 + i) * N + n) : 0.0f;
+      r_C[k] = in ? ld(p.Cc, bLN + (int64_t)(t0 + i) * N + n) : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < NPW; ++j) {
+      const int n = n0 + j;
+      r_h[j] = (valid && n < N) ? p.ckpt[(((int64_t)b * p.nblk + blk) * N + n) * D + d] : 0.0f;
+    }
+  };
+  auto commit = [&](int buf) {
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      const int i = wave + k * NG;
+      s_u[buf][i][lane] = r_u[k];
+      s_dt[buf][i][lane] = r_dt[k];
+      s_dy[buf][i][lane] = r_dy[k];
+      if (gate) {
+        s_go[buf][i][lane] = r_go[k];
+        s_gz[buf][i][lane] = r_gz[k];
+      }
+      if (stage_eu) s_eu[buf][i][lane] = r_eu[k];
+      if (stage_dyo) s_dyo[buf][i][lane] = r_dyo[k];
+    }
+#pragma unroll
+    for (int k = 0; k < BCE; ++k) {
+      const int e = threadIdx.x + k * kWave * NG;
+      if (e < kCK * NS) {
+        const int i = e / NS, n = e - (e / NS) * NS;
+        s_B[buf][i][n] = r_B[k];
+        s_C[buf][i][n] = r_C[k];
+      }
+    }
+  };
+
+  fetch(p.nblk - 1);
+  commit(0);
+  __syncthreads();
+  int buf = 0;
+  float h[NPW];
+  for (int blk = p.nblk - 1; blk >= 0; --blk, buf ^= 1) {
     const int t0 = blk * kCK;
     const int tn = min(kCK, L - t0);
-    float h[kNPW];
 #pragma unroll
-    for (int j = 0; j < kNPW; ++j) {
-      const int n = n0 + j;
-      h[j] = (valid && n < N) ? p.ckpt[(((int64_t)b * p.nblk + blk) * N + n) * D + d] : 0.0f;
-    }
-    float a_s[kCK][kNPW], hp_s[kCK][kNPW];
-    float dt_s[kCK], u_s[kCK], dy_s[kCK];
+    for (int j = 0; j < NPW; ++j) h[j] = r_h[j];
+    const bool more = blk > 0;
+    if (more) fetch(blk - 1);
 
-    // forward recompute of the block: a_t, h_{t-1}; dC_t = sum_d dy_t h_t
+    auto sweeps = [&](auto full_tag) {
+      constexpr bool kFull = decltype(full_tag)::value;
+      float a_s[kCK][NPW], hp_s[kCK][NPW];
+      float uu[kCK], dd[kCK], dyv[kCK];
 #pragma unroll
-    for (int i = 0; i < kCK; ++i) {
-      if (i < tn) {
-        const int t = t0 + i;
-        const int pt = rev ? L - 1 - t : t;
-        const float uu = valid ? ld(p.u, rowD + (int64_t)t * D + dc) : 0.0f;
-        const float dd = valid ? ld(p.delta, rowDt + (int64_t)t * dtD + dd_lane) : 0.0f;
-        const float dyv = valid ? gated_dy(p, rowD + (int64_t)pt * D + q) : 0.0f;
-        const float w = dd * uu;
-        float c[kNPW];
-        float yp = 0.0f;
+      for (int i = 0; i < kCK; ++i) {
+        if (kFull || i < tn) {
+          uu[i] = s_u[buf][i][lane];
+          dd[i] = s_dt[buf][i][lane];
+          dyv[i] = s_dy[buf][i][lane];
+        }
+      }
+      // forward recompute of the block: a_t, h_{t-1}; dC_t = sum_d dy_t h_t
 #pragma unroll
-        for (int j = 0; j < kNPW; ++j) {
-          const int n = n0 + j;
-          const float Bn = n < N ? ld(p.Bc, rowN + (int64_t)t * N + n) : 0.0f;
-          const float a = fast_exp2(A2[j] * dd);
-          a_s[i][j] = a;
-          hp_s[i][j] = h[j];
-          h[j] = fmaf(a, h[j], Bn * w);
-          c[j] = dyv * h[j];
-          if (gate) {
-            const float Cn = n < N ? ld(p.Cc, rowN + (int64_t)t * N + n) : 0.0f;
-            yp = fmaf(Cn, h[j], yp);
+      for (int i = 0; i < kCK; ++i) {
+        if (kFull || i < tn) {
+          float Bn[NPW], Cn[NPW];
+          lds_vec<NPW>(&s_B[buf][i][n0], Bn);
+          if (gate) lds_vec<NPW>(&s_C[buf][i][n0], Cn);
+          const float w = dd[i] * uu[i];
+          float c[NPW];
+          float yp = 0.0f;
+#pragma unroll
+          for (int j = 0; j < NPW; ++j) {
+            const float a = fast_exp2(A2[j] * dd[i]);
+            a_s[i][j] = a;
+            hp_s[i][j] = h[j];
+            h[j] = fmaf(a, h[j], Bn[j] * w);
+            c[j] = dyv[i] * h[j];
+            if (gate) yp = fmaf(Cn[j], h[j], yp);
           }
+          if (gate) sbuf[EPI ? 2 : 0][wave][i][lane] = yp;
+          const float r = wave_reduce<NPW>(c);
+          const int sr = wave_reduce_state<NPW>(lane);
+          if (sr >= 0) bcbuf[1][i][n0 + sr] = r;
         }
-        if (gate) sbuf[2][wave][i][lane] = yp;
-        const float r = wave_reduce4(c[0], c[1], c[2], c[3]);
-        if ((lane & 15) == 0) {
-          const int n = n0 + kRowState[lane >> 4];
-          if (n < NG * kNPW) bcbuf[1][i][n] = r;
-        }
-        dt_s[i] = dd;
-        u_s[i] = uu;
-        dy_s[i] = dyv;
       }
-    }
-
-    // adjoint, backwards through the block
+      // adjoint, backwards through the block
 #pragma unroll
-    for (int i = kCK - 1; i >= 0; --i) {
-      if (i < tn) {
-        const int t = t0 + i;
-        const float w = dt_s[i] * u_s[i];
-        float s1 = 0.0f, s2 = 0.0f;
-        float e[kNPW];
+      for (int i = kCK - 1; i >= 0; --i) {
+        if (kFull || i < tn) {
+          float Bn[NPW], Cn[NPW];
+          lds_vec<NPW>(&s_B[buf][i][n0], Bn);
+          lds_vec<NPW>(&s_C[buf][i][n0], Cn);
+          const float w = dd[i] * uu[i];
+          float s1 = 0.0f, s2 = 0.0f;
+          float e[NPW];
 #pragma unroll
-        for (int j = 0; j < kNPW; ++j) {
-          const int n = n0 + j;
-          const float Bn = n < N ? ld(p.Bc, rowN + (int64_t)t * N + n) : 0.0f;
-          const float Cn = n < N ? ld(p.Cc, rowN + (int64_t)t * N + n) : 0.0f;
-          const float f = fmaf(Cn, dy_s[i], g[j]);
-          const float gg = a_s[i][j] * f;
-          const float qv = gg * hp_s[i][j];
-          s2 = fmaf(Av[j], qv, s2);
-          dAacc[j] = fmaf(dt_s[i], qv, dAacc[j]);
-          s1 = fmaf(Bn, f, s1);
-          e[j] = f * w;
-          g[j] = gg;
+          for (int j = 0; j < NPW; ++j) {
+            const float f = fmaf(Cn[j], dyv[i], g[j]);
+            const float gg = a_s[i][j] * f;
+            const float qv = gg * hp_s[i][j];
+            s2 = fmaf(Av[j], qv, s2);
+            dAacc[j] = fmaf(dd[i], qv, dAacc[j]);
+            s1 = fmaf(Bn[j], f, s1);
+            e[j] = f * w;
+            g[j] = gg;
+          }
+          const float r = wave_reduce<NPW>(e);
+          const int sr = wave_reduce_state<NPW>(lane);
+          if (sr >= 0) bcbuf[0][i][n0 + sr] = r;
+          sbuf[0][wave][i][lane] = dd[i] * s1;
+          sbuf[1][wave][i][lane] = fmaf(uu[i], s1, s2);
         }
-        const float r = wave_reduce4(e[0], e[1], e[2], e[3]);
-        if ((lane & 15) == 0) {
-          const int n = n0 + kRowState[lane >> 4];
-          if (n < NG * kNPW) bcbuf[0][i][n] = r;
-        }
-        sbuf[0][wave][i][lane] = dt_s[i] * s1;
-        sbuf[1][wave][i][lane] = fmaf(u_s[i], s1, s2);
       }
-    }
+    };
+    if (tn == kCK) sweeps(std::true_type{}); else sweeps(std::false_type{});
     __syncthreads();
 
     // combine the per-wave partials; write du, ddelta (and dz)
@@ -380,16 +587,16 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_bwd_kernel(BwdArgs<T> p) {
         ddt += sbuf[1][w][i][lane];
       }
       const int t = t0 + i;
-      const int64_t o = rowD + (int64_t)t * D + dc;  // scan-domain (t, d)
-      if (skip && valid) {
+      const float uu = s_u[buf][i][lane];
+      if (skip) {
         // y_out[t,d] holds u[t,d]*D[d] (selectssm.py:238): its gradient lands on u[t,d]
-        const float dyo = gated_dy(p, o);
-        du = fmaf(p.Dskip[dc], dyo, du);
-        dDacc = fmaf(dyo, ld(p.u, o), dDacc);
+        const float dyo = stage_dyo ? s_dyo[buf][i][lane] : s_dy[buf][i][lane];
+        du = fmaf(Dd, dyo, du);
+        dDacc = fmaf(dyo, uu, dDacc);
       }
       if (valid) {
-        st(p.du, o, du);
-        if (p.dstride) st(p.ddelta, rowDt + (int64_t)t * dtD + dc, ddt);
+        st(p.du, bLD + (int64_t)t * D + dc, du);
+        if (p.dstride) st(p.ddelta, bLDt + (int64_t)t * dtD + dc, ddt);
       }
       if (!p.dstride) {
         const float tot = wave_sum(valid ? ddt : 0.0f);
@@ -398,27 +605,27 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_bwd_kernel(BwdArgs<T> p) {
       if (gate && valid) {
         float ys = 0.0f;
 #pragma unroll
-        for (int w = 0; w < NG; ++w) ys += sbuf[2][w][i][lane];
-        const int pt = rev ? L - 1 - t : t;
-        const int64_t oo = rowD + (int64_t)pt * D + q;  // output position of scan step (t,d)
-        if (skip) ys = fmaf(ld(p.u, oo), p.Dskip[q], ys);
-        const float zz = ld(p.z, oo);
+        for (int w = 0; w < NG; ++w) ys += sbuf[EPI ? 2 : 0][w][i][lane];
+        if (skip) ys = fmaf(stage_eu ? s_eu[buf][i][lane] : uu, Dq, ys);
+        const float zz = s_gz[buf][i][lane];
         const float sg = sigmoid(zz);
-        st(p.dz, oo, ld(p.dy, oo) * ys * sg * (1.0f + zz * (1.0f - sg)));
+        const int pt = rev ? L - 1 - t : t;
+        st(p.dz, bLD + (int64_t)pt * D + q, s_go[buf][i][lane] * ys * sg * (1.0f + zz * (1.0f - sg)));
       }
     }
     // dB, dC partials of this channel block, coalesced
     for (int idx = threadIdx.x; idx < tn * N; idx += kWave * NG) {
-      const int i = idx / N, n = idx - i * N;
+      const int i = idx / N, n = idx - (idx / N) * N;
       const int64_t o = (((int64_t)cb * p.Bt + b) * L + t0 + i) * N + n;
       p.ws_dB[o] = bcbuf[0][i][n];
       p.ws_dC[o] = bcbuf[1][i][n];
     }
+    if (more) commit(buf ^ 1);
     __syncthreads();
   }
 
 #pragma unroll
-  for (int j = 0; j < kNPW; ++j) {
+  for (int j = 0; j < NPW; ++j) {
     const int n = n0 + j;
     if (valid && n < N) p.ws_dA[((int64_t)b * D + d) * N + n] = dAacc[j];
   }
@@ -462,8 +669,22 @@ int hip_check(hipError_t e, const char* what) {
 }
 
 struct Shape {
-  int B, L, D, N, nblk, ncb, NG;
+  int B, L, D, N, nblk, ncb;
+  int NPW, NG;  // states per wave, waves per workgroup
+  bool epi;     // skip / gate epilogue fused
 };
+
+// Kernel variant for a shape: fewer states per wave give more waves per SIMD
+// (the plain scan); the fused epilogue stages more per block and keeps 4.
+void pick_variant(Shape* s, uint32_t flags) {
+  s->epi = (flags & (SSM_SKIP | SSM_GATE)) != 0;
+  s->NPW = (!s->epi && s->N <= 16) ? kPlainNPW : 4;
+  const int ng = (s->N + s->NPW - 1) / s->NPW;
+  s->NG = 1;
+  while (s->NG < ng) s->NG *= 2;  // instantiated state-group counts: 1, 2, 4, 8
+  const int ck = ck_for(s->NG, s->epi);
+  s->nblk = (s->L + ck - 1) / ck;
+}
 
 int validate(const ssm_desc_t* desc, Shape* s) {
   if (desc == nullptr) return fail(SSM_ERR_INVALID, "desc is NULL");
@@ -485,12 +706,25 @@ int validate(const ssm_desc_t* desc, Shape* s) {
   s->L = (int)desc->seqlen;
   s->D = (int)desc->dim;
   s->N = (int)desc->dstate;
-  s->nblk = (s->L + kCK - 1) / kCK;
   s->ncb = (s->D + kWave - 1) / kWave;
-  const int ng = (s->N + kNPW - 1) / kNPW;
-  s->NG = 1;
-  while (s->NG < ng) s->NG *= 2;  // instantiated state-group counts: 1, 2, 4, 8
+  pick_variant(s, desc->flags);
   return SSM_OK;
+}
+
+template <int P, int G, bool E, typename F>
+bool dispatch_one(const Shape& s, F&& f) {
+  if (s.NPW != P || s.NG != G || s.epi != E) return false;
+  f(std::integral_constant<int, P>{}, std::integral_constant<int, G>{}, std::integral_constant<bool, E>{});
+  return true;
+}
+
+// Calls f(npw, ng, epi) with the compile-time variant matching s.
+template <typename F>
+bool dispatch_variant(const Shape& s, F&& f) {
+  return dispatch_one<kPlainNPW, 1, false>(s, f) || dispatch_one<kPlainNPW, 2, false>(s, f) ||
+         dispatch_one<kPlainNPW, 4, false>(s, f) || dispatch_one<kPlainNPW, 8, false>(s, f) ||
+         (kPlainNPW != 4 && dispatch_one<4, 8, false>(s, f)) || dispatch_one<4, 1, true>(s, f) ||
+         dispatch_one<4, 2, true>(s, f) || dispatch_one<4, 4, true>(s, f) || dispatch_one<4, 8, true>(s, f);
 }
 
 size_t ckpt_floats(const Shape& s) { return (size_t)s.B * s.nblk * s.N * s.D; }
@@ -532,13 +766,12 @@ int launch_fwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const voi
   a.dstride = desc->delta_broadcast ? 0 : 1;
   a.flags = desc->flags;
   dim3 grid(s.ncb, s.B);
-  switch (s.NG) {
-    case 1: hipLaunchKernelGGL((ssm_fwd_kernel<1, T>), grid, dim3(kWave * 1), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((ssm_fwd_kernel<2, T>), grid, dim3(kWave * 2), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((ssm_fwd_kernel<4, T>), grid, dim3(kWave * 4), 0, st, a); break;
-    case 8: hipLaunchKernelGGL((ssm_fwd_kernel<8, T>), grid, dim3(kWave * 8), 0, st, a); break;
-    default: return fail(SSM_ERR_UNSUPPORTED, "unsupported state-group count");
-  }
+  if (!dispatch_variant(s, [&](auto npw, auto ng, auto epi) {
+        constexpr int P = decltype(npw)::value, G = decltype(ng)::value;
+        constexpr bool E = decltype(epi)::value;
+        hipLaunchKernelGGL((ssm_fwd_kernel<P, G, E, T>), grid, dim3(kWave * G), 0, st, a);
+      }))
+    return fail(SSM_ERR_UNSUPPORTED, "no kernel variant for this shape");
   return hip_check(hipGetLastError(), "ssm_fwd launch");
 }
 
@@ -577,13 +810,12 @@ int launch_bwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const voi
   a.dstride = bcast ? 0 : 1;
   a.flags = desc->flags;
   dim3 grid(s.ncb, s.B);
-  switch (s.NG) {
-    case 1: hipLaunchKernelGGL((ssm_bwd_kernel<1, T>), grid, dim3(kWave * 1), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((ssm_bwd_kernel<2, T>), grid, dim3(kWave * 2), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((ssm_bwd_kernel<4, T>), grid, dim3(kWave * 4), 0, st, a); break;
-    case 8: hipLaunchKernelGGL((ssm_bwd_kernel<8, T>), grid, dim3(kWave * 8), 0, st, a); break;
-    default: return fail(SSM_ERR_UNSUPPORTED, "unsupported state-group count");
-  }
+  if (!dispatch_variant(s, [&](auto npw, auto ng, auto epi) {
+        constexpr int P = decltype(npw)::value, G = decltype(ng)::value;
+        constexpr bool E = decltype(epi)::value;
+        hipLaunchKernelGGL((ssm_bwd_kernel<P, G, E, T>), grid, dim3(kWave * G), 0, st, a);
+      }))
+    return fail(SSM_ERR_UNSUPPORTED, "no kernel variant for this shape");
   int rc = hip_check(hipGetLastError(), "ssm_bwd launch");
   if (rc) return rc;
   auto reduce = [&](const float* part, auto* out, int nparts, int64_t count) {
