@@ -40,6 +40,7 @@ __host__ __device__ constexpr int ck_for(int ng, bool epi) { return (ng >= 8 && 
 #define SSM_PLAIN_NPW 2
 #endif
 constexpr int kPlainNPW = SSM_PLAIN_NPW;  // states per wave of the plain scan
+constexpr int kPF = 4;    // steps of LDS read-ahead for B, C
 constexpr int kTT = 32;   // forward time tile staged in LDS (a multiple of kCK)
 
 // ---------------------------------------------------------------- element I/O
@@ -240,48 +241,70 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_fwd_kernel(FwdArgs<T> p) {
   const int64_t bLDt = (int64_t)b * L * dtD;
   const int dd_lane = p.dstride ? dc : 0;
 
+  // uniform (b,0,0) bases; rows are added in scalar registers, the lane's
+  // channel is the only per-lane offset
+  const T* __restrict__ u_b = p.u + bLD;
+  const T* __restrict__ dt_b = p.delta + bLDt;
+  const T* __restrict__ z_b = EPI ? p.z + bLD : nullptr;
+  const T* __restrict__ B_b = p.Bc + bLN;
+  const T* __restrict__ C_b = p.Cc + bLN;
+  const int LN = L * N;
+
+  // fetch() only issues loads (clamped addresses, raw values); commit(), run
+  // after the tile's compute, zeroes what lies outside the tensor and writes
+  // LDS, so the loads' latency is covered by a whole tile.
   float r_u[RPT], r_dt[RPT], r_eu[RPT], r_ez[RPT], r_B[BCE], r_C[BCE];
   auto fetch = [&](int t0) {
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
-      const int t = t0 + wave + k * NG;
-      const bool in = valid && t < L;
-      r_u[k] = in ? ld(p.u, bLD + (int64_t)t * D + dc) : 0.0f;
-      r_dt[k] = in ? ld(p.delta, bLDt + (int64_t)t * dtD + dd_lane) : 0.0f;
-      if (stage_eu) r_eu[k] = ld_at(p.u, bLD, L, D, t, d, rev, comp);
-      if (gate) r_ez[k] = ld_at(p.z, bLD, L, D, t, d, rev, comp);
+      const int tc = min(t0 + wave + k * NG, L - 1);
+      r_u[k] = ld(u_b + (int64_t)tc * D, dc);
+      r_dt[k] = ld(dt_b + (int64_t)tc * dtD, dd_lane);
+      if (stage_eu || gate) {
+        const int pr = rev ? L - 1 - tc : tc;
+        if (stage_eu) r_eu[k] = ld(u_b + (int64_t)pr * D, q);
+        if (gate) r_ez[k] = ld(z_b + (int64_t)pr * D, q);
+      }
     }
 #pragma unroll
     for (int k = 0; k < BCE; ++k) {
       const int e = threadIdx.x + k * kWave * NG;
-      const int i = e / NS, n = e - (e / NS) * NS;
-      const bool in = e < kTT * NS && t0 + i < L && n < N;
-      r_B[k] = in ? ld(p.Bc, bLN + (int64_t)(t0 + i) * N + n) : 0.0f;
-      r_C[k] = in ? ld(p.Cc, bLN + (int64_t)(t0 + i) * N + n) : 0.0f;
+      int gi;
+      if (NS == N) {
+        gi = t0 * N + e;
+      } else {
+        const int i = e / NS, n = e - i * NS;
+        gi = (t0 + i) * N + min(n, N - 1);
+      }
+      const int gc = min(gi, LN - 1);
+      r_B[k] = ld(B_b, gc);
+      r_C[k] = ld(C_b, gc);
     }
   };
-  auto commit = [&](int buf) {
+  auto commit = [&](int buf, int t0) {
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
       const int i = wave + k * NG;
-      s_u[buf][i][lane] = r_u[k];
-      s_dt[buf][i][lane] = r_dt[k];
-      if (stage_eu) s_eu[buf][i][lane] = r_eu[k];
-      if (gate) s_ez[buf][i][lane] = r_ez[k];
+      const bool in = valid && t0 + i < L;
+      s_u[buf][i][lane] = in ? r_u[k] : 0.0f;
+      s_dt[buf][i][lane] = in ? r_dt[k] : 0.0f;
+      if (stage_eu) s_eu[buf][i][lane] = in ? r_eu[k] : 0.0f;
+      if (gate) s_ez[buf][i][lane] = in ? r_ez[k] : 0.0f;
     }
 #pragma unroll
     for (int k = 0; k < BCE; ++k) {
       const int e = threadIdx.x + k * kWave * NG;
       if (e < kTT * NS) {
-        const int i = e / NS, n = e - (e / NS) * NS;
-        s_B[buf][i][n] = r_B[k];
-        s_C[buf][i][n] = r_C[k];
+        const int i = e / NS, n = e - i * NS;
+        const bool in = t0 + i < L && n < N;
+        (&s_B[buf][0][0])[e] = in ? r_B[k] : 0.0f;
+        (&s_C[buf][0][0])[e] = in ? r_C[k] : 0.0f;
       }
     }
   };
 
   fetch(0);
-  commit(0);
+  commit(0, 0);
   __syncthreads();
   int buf = 0;
   for (int t0 = 0; t0 < L; t0 += kTT, buf ^= 1) {
@@ -299,12 +322,25 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_fwd_kernel(FwdArgs<T> p) {
           dd[i] = s_dt[buf][i][lane];
         }
       }
+      // B, C of step i+kPF are read while step i computes (ring of kPF+1)
+      float Br[kPF + 1][NPW], Cr[kPF + 1][NPW];
+#pragma unroll
+      for (int i = 0; i < kPF; ++i) {
+        if (kFull || i < tn) {
+          lds_vec<NPW>(&s_B[buf][i][n0], Br[i]);
+          lds_vec<NPW>(&s_C[buf][i][n0], Cr[i]);
+        }
+      }
 #pragma unroll
       for (int i = 0; i < kTT; ++i) {
         if (kFull || i < tn) {
-          float Bn[NPW], Cn[NPW];
-          lds_vec<NPW>(&s_B[buf][i][n0], Bn);
-          lds_vec<NPW>(&s_C[buf][i][n0], Cn);
+          if (i + kPF < kTT && (kFull || i + kPF < tn)) {
+            lds_vec<NPW>(&s_B[buf][i + kPF][n0], Br[(i + kPF) % (kPF + 1)]);
+            lds_vec<NPW>(&s_C[buf][i + kPF][n0], Cr[(i + kPF) % (kPF + 1)]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          const float* Bn = Br[i % (kPF + 1)];
+          const float* Cn = Cr[i % (kPF + 1)];
           if (p.ckpt != nullptr && (i % kCK) == 0) {
             const int blk = (t0 + i) / kCK;
 #pragma unroll
@@ -345,7 +381,7 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_fwd_kernel(FwdArgs<T> p) {
         st(p.y, bLD + (int64_t)pt * D + q, ys);
       }
     }
-    if (more) commit(buf ^ 1);
+    if (more) commit(buf ^ 1, t0 + kTT);
     __syncthreads();
   }
 }
@@ -428,76 +464,93 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_bwd_kernel(BwdArgs<T> p) {
   const int64_t bLDt = (int64_t)b * L * dtD;
   const int dd_lane = p.dstride ? dc : 0;
 
-  float r_u[RPT], r_dt[RPT], r_dy[RPT], r_go[RPT], r_gz[RPT], r_eu[RPT], r_dyo[RPT];
+  const T* __restrict__ u_b = p.u + bLD;
+  const T* __restrict__ dt_b = p.delta + bLDt;
+  const T* __restrict__ dy_b = p.dy + bLD;
+  const T* __restrict__ z_b = EPI ? p.z + bLD : nullptr;
+  const T* __restrict__ B_b = p.Bc + bLN;
+  const T* __restrict__ C_b = p.Cc + bLN;
+  const float* __restrict__ ck_b = p.ckpt + (int64_t)b * p.nblk * N * D;
+  const int LN = L * N;
+
+  // fetch() only issues loads; commit() (after the block's compute) masks,
+  // applies the gate and writes LDS
+  float r_u[RPT], r_dt[RPT], r_dy[RPT], r_gz[RPT], r_eu[RPT], r_dyo[RPT], r_zo[RPT];
   float r_B[BCE], r_C[BCE], r_h[NPW];
   auto fetch = [&](int blk) {
     const int t0 = blk * kCK;
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
-      const int t = t0 + wave + k * NG;
-      const bool in = valid && t < L;
-      r_u[k] = in ? ld(p.u, bLD + (int64_t)t * D + dc) : 0.0f;
-      r_dt[k] = in ? ld(p.delta, bLDt + (int64_t)t * dtD + dd_lane) : 0.0f;
-      const float go = ld_at(p.dy, bLD, L, D, t, d, rev, comp);
-      if (gate) {
-        const float gz = ld_at(p.z, bLD, L, D, t, d, rev, comp);
-        r_go[k] = go;
-        r_gz[k] = gz;
-        r_dy[k] = go * gz * sigmoid(gz);
-      } else {
-        r_dy[k] = go;
-      }
-      if (stage_eu) r_eu[k] = ld_at(p.u, bLD, L, D, t, d, rev, comp);
+      const int tc = min(t0 + wave + k * NG, L - 1);
+      const int pr = rev ? L - 1 - tc : tc;  // output row of scan step tc
+      r_u[k] = ld(u_b + (int64_t)tc * D, dc);
+      r_dt[k] = ld(dt_b + (int64_t)tc * dtD, dd_lane);
+      r_dy[k] = ld(dy_b + (int64_t)pr * D, q);
+      if (gate) r_gz[k] = ld(z_b + (int64_t)pr * D, q);
+      if (stage_eu) r_eu[k] = ld(u_b + (int64_t)pr * D, q);
       if (stage_dyo) {
-        float v = ld_at(p.dy, bLD, L, D, t, d, false, false);
-        if (gate) {
-          const float zz = ld_at(p.z, bLD, L, D, t, d, false, false);
-          v *= zz * sigmoid(zz);
-        }
-        r_dyo[k] = v;
+        r_dyo[k] = ld(dy_b + (int64_t)tc * D, dc);
+        if (gate) r_zo[k] = ld(z_b + (int64_t)tc * D, dc);
       }
     }
 #pragma unroll
     for (int k = 0; k < BCE; ++k) {
       const int e = threadIdx.x + k * kWave * NG;
-      const int i = e / NS, n = e - (e / NS) * NS;
-      const bool in = e < kCK * NS && t0 + i < L && n < N;
-      r_B[k] = in ? ld(p.Bc, bLN + (int64_t)(t0 + i) * N + n) : 0.0f;
-      r_C[k] = in ? ld(p.Cc, bLN + (int64_t)(t0 + i) * N + n) : 0.0f;
+      int gi;
+      if (NS == N) {
+        gi = t0 * N + e;
+      } else {
+        const int i = e / NS, n = e - i * NS;
+        gi = (t0 + i) * N + min(n, N - 1);
+      }
+      const int gc = min(gi, LN - 1);
+      r_B[k] = ld(B_b, gc);
+      r_C[k] = ld(C_b, gc);
     }
 #pragma unroll
-    for (int j = 0; j < NPW; ++j) {
-      const int n = n0 + j;
-      r_h[j] = (valid && n < N) ? p.ckpt[(((int64_t)b * p.nblk + blk) * N + n) * D + d] : 0.0f;
-    }
+    for (int j = 0; j < NPW; ++j) r_h[j] = ck_b[((int64_t)blk * N + min(n0 + j, N - 1)) * D + dc];
   };
-  auto commit = [&](int buf) {
+  auto commit = [&](int buf, int blk) {
+    const int t0 = blk * kCK;
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
       const int i = wave + k * NG;
-      s_u[buf][i][lane] = r_u[k];
-      s_dt[buf][i][lane] = r_dt[k];
-      s_dy[buf][i][lane] = r_dy[k];
+      const bool in = valid && t0 + i < L;
+      s_u[buf][i][lane] = in ? r_u[k] : 0.0f;
+      s_dt[buf][i][lane] = in ? r_dt[k] : 0.0f;
+      const float go = in ? r_dy[k] : 0.0f;
       if (gate) {
-        s_go[buf][i][lane] = r_go[k];
-        s_gz[buf][i][lane] = r_gz[k];
+        const float gz = in ? r_gz[k] : 0.0f;
+        s_go[buf][i][lane] = go;
+        s_gz[buf][i][lane] = gz;
+        s_dy[buf][i][lane] = go * gz * sigmoid(gz);
+      } else {
+        s_dy[buf][i][lane] = go;
       }
-      if (stage_eu) s_eu[buf][i][lane] = r_eu[k];
-      if (stage_dyo) s_dyo[buf][i][lane] = r_dyo[k];
+      if (stage_eu) s_eu[buf][i][lane] = in ? r_eu[k] : 0.0f;
+      if (stage_dyo) {
+        float v = in ? r_dyo[k] : 0.0f;
+        if (gate) {
+          const float zz = r_zo[k];
+          v *= zz * sigmoid(zz);
+        }
+        s_dyo[buf][i][lane] = v;
+      }
     }
 #pragma unroll
     for (int k = 0; k < BCE; ++k) {
       const int e = threadIdx.x + k * kWave * NG;
       if (e < kCK * NS) {
-        const int i = e / NS, n = e - (e / NS) * NS;
-        s_B[buf][i][n] = r_B[k];
-        s_C[buf][i][n] = r_C[k];
+        const int i = e / NS, n = e - i * NS;
+        const bool in = t0 + i < L && n < N;
+        (&s_B[buf][0][0])[e] = in ? r_B[k] : 0.0f;
+        (&s_C[buf][0][0])[e] = in ? r_C[k] : 0.0f;
       }
     }
   };
 
   fetch(p.nblk - 1);
-  commit(0);
+  commit(0, p.nblk - 1);
   __syncthreads();
   int buf = 0;
   float h[NPW];
@@ -505,7 +558,7 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_bwd_kernel(BwdArgs<T> p) {
     const int t0 = blk * kCK;
     const int tn = min(kCK, L - t0);
 #pragma unroll
-    for (int j = 0; j < NPW; ++j) h[j] = r_h[j];
+    for (int j = 0; j < NPW; ++j) h[j] = (valid && n0 + j < N) ? r_h[j] : 0.0f;
     const bool more = blk > 0;
     if (more) fetch(blk - 1);
 
@@ -614,13 +667,23 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_bwd_kernel(BwdArgs<T> p) {
       }
     }
     // dB, dC partials of this channel block, coalesced
-    for (int idx = threadIdx.x; idx < tn * N; idx += kWave * NG) {
-      const int i = idx / N, n = idx - (idx / N) * N;
-      const int64_t o = (((int64_t)cb * p.Bt + b) * L + t0 + i) * N + n;
-      p.ws_dB[o] = bcbuf[0][i][n];
-      p.ws_dC[o] = bcbuf[1][i][n];
+    {
+      float* __restrict__ wB = p.ws_dB + (((int64_t)cb * p.Bt + b) * L + t0) * N;
+      float* __restrict__ wC = p.ws_dC + (((int64_t)cb * p.Bt + b) * L + t0) * N;
+      for (int idx = threadIdx.x; idx < tn * N; idx += kWave * NG) {
+        int i, n;
+        if (NS == N) {
+          i = idx / NS;
+          n = idx - i * NS;
+        } else {
+          i = idx / N;
+          n = idx - i * N;
+        }
+        wB[idx] = bcbuf[0][i][n];
+        wC[idx] = bcbuf[1][i][n];
+      }
     }
-    if (more) commit(buf ^ 1);
+    if (more) commit(buf ^ 1, blk - 1);
     __syncthreads();
   }
 
