@@ -1,0 +1,78 @@
+"""The C ABI library loads, exports every function include/selectssm.h declares and
+rejects invalid requests with error codes (no GPU work is launched here)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from selectssm_amd import _lib as L
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "selectssm.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ssm_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_bound_symbols():
+    assert header_functions() == sorted(L.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = L.lib()
+    for name in header_functions():
+        assert hasattr(lib, name), name
+    assert lib.ssm_abi_version() == L.ABI_VERSION
+
+
+def test_header_constants_match_binding():
+    text = open(HEADER).read()
+    consts = dict(re.findall(r"#define (SSM_\w+) (\d+)u?", text))
+    for k in ("SSM_OK", "SSM_ERR_INVALID", "SSM_ERR_UNSUPPORTED", "SSM_ERR_HIP", "SSM_F32", "SSM_BF16",
+              "SSM_REVERSE", "SSM_COMPLEMENT", "SSM_SKIP", "SSM_GATE"):
+        assert int(consts[k]) == getattr(L, k), k
+    assert int(consts["SSM_ABI_VERSION"]) == L.ABI_VERSION
+    assert ctypes.sizeof(L.SsmDesc) == 48
+
+
+def test_size_queries():
+    lib = L.lib()
+    d = L.make_desc(8, 8192, 2048, 16)
+    # checkpoints: one f32 state per (b, block of 16 steps, n, d)
+    assert lib.ssm_ckpt_bytes(ctypes.byref(d)) == 8 * (8192 // 16) * 16 * 2048 * 4
+    assert lib.ssm_bwd_workspace_bytes(ctypes.byref(d)) > 0
+    bad = L.make_desc(8, 8192, 2048, 33)
+    assert lib.ssm_ckpt_bytes(ctypes.byref(bad)) == 0
+    assert b"dstate" in lib.ssm_last_error()
+
+
+@pytest.mark.parametrize("field,value,msg", [
+    ("batch", 0, b"batch, seqlen and dim"), ("dstate", 0, b"dstate"), ("dtype", 7, b"dtype"),
+    ("flags", 64, b"unknown flag"), ("flags", 2, b"COMPLEMENT requires"), ("delta_broadcast", 3, b"delta_broadcast"),
+    ("reserved", 1, b"reserved"),
+])
+def test_invalid_desc_is_rejected_before_any_launch(field, value, msg):
+    lib = L.lib()
+    d = L.make_desc(2, 64, 64, 16)
+    setattr(d, field, value)
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    rc = lib.ssm_fwd(None, ctypes.byref(d), p, p, p, p, p, None, None, p, None)
+    assert rc == L.SSM_ERR_INVALID
+    assert msg in lib.ssm_last_error()
+
+
+def test_null_pointers_and_missing_epilogue_operands_are_rejected():
+    lib = L.lib()
+    d = L.make_desc(2, 64, 64, 16)
+    p = ctypes.c_void_p(16)
+    assert lib.ssm_fwd(None, ctypes.byref(d), None, p, p, p, p, None, None, p, None) == L.SSM_ERR_INVALID
+    d.flags = L.SSM_SKIP
+    assert lib.ssm_fwd(None, ctypes.byref(d), p, p, p, p, p, None, None, p, None) == L.SSM_ERR_INVALID
+    assert b"Dskip" in lib.ssm_last_error()
+    d.flags = L.SSM_GATE
+    rc = lib.ssm_bwd(None, ctypes.byref(d), p, p, p, p, p, None, p, p, p, p, p, p, p, p, None, None, p)
+    assert rc == L.SSM_ERR_INVALID and b"dz" in lib.ssm_last_error()
+    assert lib.ssm_fwd(None, None, p, p, p, p, p, None, None, p, None) == L.SSM_ERR_INVALID

@@ -1,0 +1,318 @@
+"""Pins the CPU oracle (oracle/ssm_oracle.py, oracle/ssm_oracle.c) without the reference.
+
+The reference (JAX/Flax) cannot be imported here and holds no golden vectors,
+so each oracle function is checked against something independent of its own
+formula: a library routine (scipy.signal.lfilter, numpy.convolve), a
+different closed form (explicit double sums), special cases, torch.autograd on
+an independent restatement, finite differences, and the restatements of the
+reference's own algorithms (chunked / recursive / custom VJP) against each
+other.  Each check is chosen so a plausible slip (a dropped term, an
+off-by-one in the decay product, a wrong sign, transposed operands) fails it.
+"""
+import math
+
+import numpy as np
+import pytest
+import scipy.signal
+
+from oracle import ssm_oracle as O
+from selectssm_amd.synthetic import make_inputs
+
+
+def _rand(shape, seed, N=None):
+    Bt, L, D, N = shape
+    return make_inputs(Bt, L, D, N, seed=seed, dtype=np.float64)
+
+
+# ------------------------------------------------------------------ forward
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_forward_lti_equals_lfilter(seed):
+    """Constant dt, B, C over time: each state is a first-order IIR filter of u."""
+    rng = np.random.default_rng(seed)
+    Bt, L, D, N = 2, 300, 5, 4
+    u = rng.standard_normal((Bt, L, D))
+    A = -np.exp(rng.uniform(0, np.log(16), (D, N)))
+    dt_d = rng.uniform(0.01, 0.3, (Bt, D))
+    Bn = rng.standard_normal((Bt, N))
+    Cn = rng.standard_normal((Bt, N))
+    delta = np.broadcast_to(dt_d[:, None, :], (Bt, L, D)).copy()
+    Bc = np.broadcast_to(Bn[:, None, :], (Bt, L, N)).copy()
+    Cc = np.broadcast_to(Cn[:, None, :], (Bt, L, N)).copy()
+    y = O.scan_forward(u, delta, A, Bc, Cc)
+    ref = np.zeros_like(y)
+    for b in range(Bt):
+        for d in range(D):
+            for n in range(N):
+                a = math.exp(A[d, n] * dt_d[b, d])
+                h = scipy.signal.lfilter([Bn[b, n] * dt_d[b, d]], [1.0, -a], u[b, :, d])
+                ref[b, :, d] += Cn[b, n] * h
+    np.testing.assert_allclose(y, ref, rtol=1e-12, atol=1e-12)
+
+
+def _brute_forward(u, delta, A, B, C):
+    """y_t = sum_n C_t,n sum_{s<=t} (prod_{s<r<=t} a_r,n) B_s,n dt_s u_s, expanded."""
+    Bt, L, D = u.shape
+    N = A.shape[1]
+    y = np.zeros((Bt, L, D))
+    for b in range(Bt):
+        for d in range(D):
+            for n in range(N):
+                a = np.exp(A[d, n] * delta[b, :, d])
+                for t in range(L):
+                    acc = 0.0
+                    for s in range(t + 1):
+                        acc += np.prod(a[s + 1:t + 1]) * B[b, s, n] * delta[b, s, d] * u[b, s, d]
+                    y[b, t, d] += C[b, t, n] * acc
+    return y
+
+
+@pytest.mark.parametrize("shape", [(1, 8, 3, 2), (2, 13, 2, 3)])
+def test_forward_equals_brute_force_sum(shape):
+    x = _rand(shape, 3)
+    y = O.scan_forward(x["u"], x["dt"], x["A"], x["B"], x["C"])
+    np.testing.assert_allclose(y, _brute_forward(x["u"], x["dt"], x["A"], x["B"], x["C"]), rtol=1e-12, atol=1e-14)
+
+
+def test_forward_special_cases():
+    x = _rand((2, 40, 6, 4), 4)
+    u, dt, A, B, C = x["u"], x["dt"], x["A"], x["B"], x["C"]
+    assert np.all(O.scan_forward(u, 0 * dt, A, B, C) == 0)          # dt = 0: no input, no decay
+    assert np.all(O.scan_forward(u, dt, A, 0 * B, C) == 0)           # B = 0
+    # A -> -inf: a = 0, memoryless: y_t = sum_n C B dt u
+    y = O.scan_forward(u, dt, np.full_like(A, -1e300), B, C)
+    ref = np.einsum("bln,bln->bl", C, B)[..., None] * dt * u
+    np.testing.assert_allclose(y, ref, rtol=1e-13, atol=1e-15)
+    # C = e_n isolates state n: h_t = a h + B dt u, recursion unrolled by hand
+    n = 2
+    e = np.zeros_like(C)
+    e[..., n] = 1.0
+    y = O.scan_forward(u, dt, A, B, e)
+    h = np.zeros((2, 6))
+    for t in range(40):
+        h = np.exp(A[:, n][None] * dt[:, t]) * h + B[:, t, n][:, None] * dt[:, t] * u[:, t]
+        np.testing.assert_allclose(y[:, t], h, rtol=1e-13, atol=1e-15)
+
+
+def test_forward_linear_and_causal():
+    x = _rand((2, 50, 4, 3), 5)
+    u2 = np.random.default_rng(9).standard_normal(x["u"].shape)
+    f = lambda uu: O.scan_forward(uu, x["dt"], x["A"], x["B"], x["C"])
+    np.testing.assert_allclose(f(2.0 * x["u"] - 3.0 * u2), 2.0 * f(x["u"]) - 3.0 * f(u2), rtol=1e-11, atol=1e-13)
+    up = x["u"].copy()
+    up[:, 30] += 1.0
+    assert np.array_equal(f(up)[:, :30], f(x["u"])[:, :30])
+    assert not np.allclose(f(up)[:, 30:], f(x["u"])[:, 30:])
+
+
+def test_forward_broadcast_delta():
+    x = _rand((2, 30, 5, 3), 6)
+    dt1 = x["dt"][..., :1]
+    y1 = O.scan_forward(x["u"], dt1, x["A"], x["B"], x["C"])
+    yf = O.scan_forward(x["u"], np.repeat(dt1, 5, axis=-1), x["A"], x["B"], x["C"])
+    np.testing.assert_array_equal(y1, yf)
+
+
+# ----------------------------------------------------------------- backward
+
+def _torch_forward(u, dt, A, B, C):
+    """Independent restatement: cumulative-log-decay form, materialised over (t, s)."""
+    import torch
+
+    L = u.shape[1]
+    la = A[None, None] * dt[..., None]                       # (B,L,D,N) log a_t
+    cum = torch.cumsum(la, dim=1)                            # sum_{r<=t} log a_r
+    beta = B[:, :, None, :] * (dt * u)[..., None]            # (B,L,D,N)
+    # h_t = sum_{s<=t} exp(cum_t - cum_s) beta_s
+    w = torch.exp(cum[:, :, None] - cum[:, None, :])         # (B,t,s,D,N)
+    mask = torch.tril(torch.ones(L, L, dtype=torch.bool))[None, :, :, None, None]
+    h = (torch.where(mask, w, torch.zeros_like(w)) * beta[:, None]).sum(2)
+    return torch.einsum("bldn,bln->bld", h, C)
+
+
+@pytest.mark.parametrize("shape,bcast", [((2, 12, 3, 4), False), ((1, 20, 5, 2), False), ((2, 9, 4, 3), True)])
+def test_backward_equals_torch_autograd(shape, bcast):
+    torch = pytest.importorskip("torch")
+    x = make_inputs(*shape, seed=7, dtype=np.float64, delta_broadcast=bcast)
+    t = {k: torch.tensor(x[k], requires_grad=True) for k in ("u", "dt", "A", "B", "C")}
+    y = _torch_forward(t["u"], t["dt"].expand(*shape[:3]) if bcast else t["dt"], t["A"], t["B"], t["C"])
+    np.testing.assert_allclose(y.detach().numpy(), O.scan_forward(x["u"], x["dt"], x["A"], x["B"], x["C"]),
+                               rtol=1e-10, atol=1e-13)
+    (y * torch.tensor(x["g"])).sum().backward()
+    got = O.scan_backward(x["u"], x["dt"], x["A"], x["B"], x["C"], x["g"])
+    for name, gg in zip(("u", "dt", "A", "B", "C"), got):
+        np.testing.assert_allclose(gg, t[name].grad.numpy(), rtol=1e-9, atol=1e-12, err_msg=name)
+
+
+def test_backward_finite_differences():
+    x = _rand((1, 10, 3, 3), 8)
+    keys = ("u", "dt", "A", "B", "C")
+    grads = dict(zip(keys, O.scan_backward(x["u"], x["dt"], x["A"], x["B"], x["C"], x["g"])))
+    loss = lambda xx: float(np.sum(O.scan_forward(*(xx[k] for k in keys)) * x["g"]))
+    rng = np.random.default_rng(0)
+    for k in keys:
+        v = rng.standard_normal(x[k].shape)
+        eps = 1e-6
+        xp = dict(x)
+        xm = dict(x)
+        xp[k] = x[k] + eps * v
+        xm[k] = x[k] - eps * v
+        fd = (loss(xp) - loss(xm)) / (2 * eps)
+        assert abs(fd - np.sum(grads[k] * v)) <= 1e-6 * max(1.0, abs(fd)), k
+
+
+# ------------------------------------------------ reference-algorithm restatements
+
+def test_associative_scan_equals_sequential_fold():
+    rng = np.random.default_rng(1)
+    for n in list(range(1, 40)) + [64, 97]:
+        g = rng.uniform(0.1, 1.0, (n, 3))
+        h = rng.standard_normal((n, 3))
+        gs, hs = O.associative_scan(O._combine, [g, h])
+        G, H = np.ones(3), np.zeros(3)
+        for i in range(n):
+            G, H = G * g[i], g[i] * H + h[i]
+            np.testing.assert_allclose(gs[i], G, rtol=1e-13)
+            np.testing.assert_allclose(hs[i], H, rtol=1e-12, atol=1e-14)
+
+
+@pytest.mark.parametrize("L,cs,K", [(96, None, 1), (96, 8, 2), (96, 1, 1), (96, 96, 4), (100, None, 2), (64, 16, 8)])
+def test_chunked_scan_restatement(L, cs, K):
+    x = _rand((2, L, 8, 4), 10)
+    ref = O.scan_forward(x["u"], x["dt"], x["A"], x["B"], x["C"])
+    y64 = O.chunked_scan(x["u"], x["dt"], x["A"], x["B"], x["C"], cs, K, dtype=np.float64)
+    np.testing.assert_allclose(y64, ref, rtol=1e-12, atol=1e-15)
+    y32 = O.chunked_scan(x["u"], x["dt"], x["A"], x["B"], x["C"], cs, K, dtype=np.float32)
+    np.testing.assert_allclose(y32, ref, rtol=1e-4, atol=1e-6)
+
+
+@pytest.mark.parametrize("L,ml,sp", [(96, 2, 2), (1000, 2, 2), (64, 3, 4), (81, 2, 3), (7, 2, 2), (1, 2, 2)])
+def test_recursive_scan_and_custom_vjp_restatements(L, ml, sp):
+    x = _rand((2, L, 5, 3), 11)
+    args = (x["u"], x["dt"], x["A"], x["B"], x["C"])
+    np.testing.assert_allclose(O.recursive_scan(*args, ml, sp, dtype=np.float64), O.scan_forward(*args),
+                               rtol=1e-12, atol=1e-15)
+    got = O.recursive_scan_backward(*args, x["g"], ml, sp, dtype=np.float64)
+    ref = O.scan_backward(*args, x["g"])
+    for a, r, name in zip(got, ref, ("du", "ddt", "dA", "dB", "dC")):
+        np.testing.assert_allclose(a, r, rtol=1e-11, atol=1e-14, err_msg=name)
+
+
+# ------------------------------------------------------------- chunk rule (A1)
+
+def _brute_chunk(L, K):
+    b = int(math.sqrt(K * L))
+    return max(c for c in range(1, L + 1) if L % c == 0 and c <= b) if L >= 2 else L
+
+
+def test_chunk_rule_brute_force_and_known_values():
+    from selectssm_amd.scan import resolve_chunking
+
+    for L in range(1, 601):
+        for K in range(1, 9):
+            want = _brute_chunk(L, K)
+            assert O.resolve_chunking(L, 8 * K, None, K)[0] == want
+            assert resolve_chunking(L, 8 * K, None, K)[0] == want
+    known = {1024: 32, 8192: 64, 131072: 256, 1048576: 1024, 4096: 64, 1000: 25, 96: 8}
+    for L, c in known.items():
+        assert O.resolve_chunking(L, 64)[0] == c
+        assert resolve_chunking(L, 64)[0] == c
+    assert O.resolve_chunking(96, 64, None, None) == (8, 1)
+
+
+def test_chunk_rule_errors_match_reference_messages():
+    from selectssm_amd.scan import resolve_chunking
+
+    for f in (O.resolve_chunking, resolve_chunking):
+        with pytest.raises(ValueError, match=r"n_channel_groups=3 must divide D=64"):
+            f(96, 64, None, 3)
+        with pytest.raises(ValueError, match=r"chunk_size=7 must divide L=96"):
+            f(96, 64, 7, 1)
+
+
+# ------------------------------------------------------ epilogue, flips, conv
+
+def test_block_forward_reverse_skip_quirk_and_gate():
+    x = _rand((2, 20, 6, 3), 12)
+    u, dt, A, B, C, D, z = (x[k] for k in ("u", "dt", "A", "B", "C", "D", "z"))
+    D = D * np.linspace(0.5, 1.5, 6)
+    ys = O.scan_forward(u, dt, A, B, C)
+    silu = z / (1 + np.exp(-z))
+    # reverse: y_out[p] = y_scan[L-1-p] + u[p] * D   (u stays in the scan domain)
+    got = O.ssm_block_forward(u, dt, A, B, C, Dskip=D, reverse=True)
+    np.testing.assert_allclose(got, ys[:, ::-1, :] + u * D, rtol=1e-13)
+    # complement: y_out[p, q] = y_scan[L-1-p, D-1-q] + u[p, q] * D[q]
+    got = O.ssm_block_forward(u, dt, A, B, C, Dskip=D, z=z, reverse=True, complement=True)
+    np.testing.assert_allclose(got, (ys[:, ::-1, ::-1] + u * D) * silu, rtol=1e-13)
+    # the flip is an involution and equals the RC action of rcps.py:10-13
+    assert np.array_equal(O.flip_domain(O.flip_domain(u, True), True), u)
+    assert O.flip_domain(u, True)[1, 0, 0] == u[1, -1, -1]
+
+
+@pytest.mark.parametrize("flags", [dict(), dict(skip=1), dict(gate=1), dict(skip=1, gate=1, reverse=1),
+                                   dict(skip=1, gate=1, reverse=1, complement=1)])
+def test_block_backward_finite_differences(flags):
+    x = _rand((1, 9, 4, 2), 13)
+    x["D"] = x["D"] * np.linspace(0.5, 1.5, 4)
+    kw = dict(Dskip=x["D"] if flags.get("skip") else None, z=x["z"] if flags.get("gate") else None,
+              reverse=bool(flags.get("reverse")), complement=bool(flags.get("complement")))
+    keys = ["u", "dt", "A", "B", "C"]
+    grads = O.ssm_block_backward(x["u"], x["dt"], x["A"], x["B"], x["C"], x["g"], **kw)
+    named = dict(zip(keys + ["D", "z"], grads))
+    if kw["Dskip"] is not None:
+        keys.append("D")
+    if kw["z"] is not None:
+        keys.append("z")
+
+    def loss(xx):
+        kk = dict(kw)
+        if kk["Dskip"] is not None:
+            kk["Dskip"] = xx["D"]
+        if kk["z"] is not None:
+            kk["z"] = xx["z"]
+        return float(np.sum(O.ssm_block_forward(xx["u"], xx["dt"], xx["A"], xx["B"], xx["C"], **kk) * x["g"]))
+
+    rng = np.random.default_rng(1)
+    for k in keys:
+        v = rng.standard_normal(x[k].shape)
+        eps = 1e-6
+        xp, xm = dict(x), dict(x)
+        xp[k] = x[k] + eps * v
+        xm[k] = x[k] - eps * v
+        fd = (loss(xp) - loss(xm)) / (2 * eps)
+        assert abs(fd - np.sum(named[k] * v)) <= 1e-6 * max(1.0, abs(fd)), k
+
+
+def test_causal_conv1d_equals_numpy_convolve_and_fd():
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((2, 30, 5))
+    w = rng.standard_normal((4, 5))
+    u = O.causal_conv1d(x, w)
+    for b in range(2):
+        for d in range(5):
+            np.testing.assert_allclose(u[b, :, d], np.convolve(x[b, :, d], w[::-1, d])[:30], rtol=1e-13, atol=1e-14)
+    g = rng.standard_normal(u.shape)
+    dx, dw = O.conv1d_silu_backward(x, w, g)
+    loss = lambda xx, ww: float(np.sum(O.conv1d_silu(xx, ww) * g))
+    vx, vw = rng.standard_normal(x.shape), rng.standard_normal(w.shape)
+    eps = 1e-6
+    fd = (loss(x + eps * vx, w + eps * vw) - loss(x - eps * vx, w - eps * vw)) / (2 * eps)
+    np.testing.assert_allclose(fd, np.sum(dx * vx) + np.sum(dw * vw), rtol=1e-6)
+
+
+# --------------------------------------------------------------- C restatement
+
+@pytest.mark.parametrize("shape,ml,sp", [((2, 96, 8, 4), 2, 2), ((2, 1000, 16, 16), 2, 2), ((1, 64, 5, 3), 3, 4),
+                                         ((3, 37, 9, 16), 2, 2), ((1, 1, 4, 2), 2, 2)])
+def test_c_port_matches_numpy_oracle(shape, ml, sp):
+    from oracle import c_oracle
+
+    x = make_inputs(*shape, seed=0)
+    args = (x["u"], x["dt"], x["A"], x["B"], x["C"])
+    y = c_oracle.scan_fwd(*args, ml, sp, nthreads=2)
+    yr = O.scan_forward(*args)
+    np.testing.assert_allclose(y, yr, rtol=1e-4, atol=1e-6)
+    got = c_oracle.scan_bwd(*args, x["g"], ml, sp, nthreads=2)
+    ref = O.scan_backward(*args, x["g"])
+    for a, r, name in zip(got, ref, ("du", "ddt", "dA", "dB", "dC")):
+        np.testing.assert_allclose(a, r, rtol=1e-4, atol=1e-5, err_msg=name)
