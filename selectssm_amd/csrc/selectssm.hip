@@ -60,6 +60,12 @@ __device__ __forceinline__ float ld<bf16>(const bf16* p, int64_t i) {
   return __uint_as_float(static_cast<uint32_t>(p[i].bits) << 16);
 }
 
+// element at a 32-bit unsigned offset from a (wave-uniform) base pointer
+template <typename T>
+__device__ __forceinline__ float ld32(const T* base, uint32_t off) {
+  return ld(reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + (size_t)off * sizeof(T)), 0);
+}
+
 template <typename T>
 __device__ __forceinline__ void st(T* p, int64_t i, float v);
 template <>
@@ -128,6 +134,35 @@ __device__ __forceinline__ float wave_sum(float v) {
   v += __shfl_xor(v, 16);
   v += __shfl_xor(v, 32);
   return v;
+}
+
+// Eight per-lane values over all 64 lanes.  Lane l ends with the total of
+// x[wave_reduce8_index(l)]; the 8 lanes of each group of 8 hold the same one.
+__device__ __forceinline__ float wave_reduce8(const float (&x)[8]) {
+  float p[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {  // lanes < 32 keep x[2m], lanes >= 32 keep x[2m+1]
+    auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[2 * m]), __float_as_uint(x[2 * m + 1]), false, false);
+    p[m] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  }
+  float q[2];
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {  // rows 0..3 keep p[2m](r0+r1), p[2m+1](r0+r1), p[2m](r2+r3), p[2m+1](r2+r3)
+    auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(p[2 * m]), __float_as_uint(p[2 * m + 1]), false, false);
+    q[m] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  }
+  // lanes with bit 3 clear keep q[0], set keep q[1]; the partner 8 lanes away adds its copy
+  const bool hi = (__lane_id() & 8) != 0;
+  const float keep = hi ? q[1] : q[0];
+  const float give = hi ? q[0] : q[1];
+  float r = keep + dpp_move<0x128>(give);  // row_ror:8
+  r += dpp_move<0xB1>(r);                  // quad_perm [1,0,3,2]
+  r += dpp_move<0x4E>(r);                  // quad_perm [2,3,0,1]
+  r += dpp_move<0x141>(r);                 // row_half_mirror
+  return r;
+}
+__device__ __forceinline__ int wave_reduce8_index(int lane) {
+  return 4 * ((lane >> 3) & 1) + ((0x3120 >> (4 * (lane >> 4))) & 0xf);
 }
 
 // Sum over the wave of each of the NPW per-lane values.  The totals land in a
@@ -258,12 +293,12 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_fwd_kernel(FwdArgs<T> p) {
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
       const int tc = min(t0 + wave + k * NG, L - 1);
-      r_u[k] = ld(u_b + (int64_t)tc * D, dc);
-      r_dt[k] = ld(dt_b + (int64_t)tc * dtD, dd_lane);
+      r_u[k] = ld32(u_b, (uint32_t)(tc * D + dc));
+      r_dt[k] = ld32(dt_b, (uint32_t)(tc * dtD + dd_lane));
       if (stage_eu || gate) {
         const int pr = rev ? L - 1 - tc : tc;
-        if (stage_eu) r_eu[k] = ld(u_b + (int64_t)pr * D, q);
-        if (gate) r_ez[k] = ld(z_b + (int64_t)pr * D, q);
+        if (stage_eu) r_eu[k] = ld32(u_b, (uint32_t)(pr * D + q));
+        if (gate) r_ez[k] = ld32(z_b, (uint32_t)(pr * D + q));
       }
     }
 #pragma unroll
@@ -277,8 +312,8 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_fwd_kernel(FwdArgs<T> p) {
         gi = (t0 + i) * N + min(n, N - 1);
       }
       const int gc = min(gi, LN - 1);
-      r_B[k] = ld(B_b, gc);
-      r_C[k] = ld(C_b, gc);
+      r_B[k] = ld32(B_b, (uint32_t)gc);
+      r_C[k] = ld32(C_b, (uint32_t)gc);
     }
   };
   auto commit = [&](int buf, int t0) {
@@ -417,6 +452,8 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_bwd_kernel(BwdArgs<T> p) {
   constexpr int kCK = ck_for(NG, EPI);
   constexpr int NS = NG * NPW;
   constexpr int RPT = kCK / NG;
+  constexpr int kRB = 8 / NPW;  // steps per batched dB / dC reduction
+  static_assert(kCK % kRB == 0, "reduction batches must tile the block");
   constexpr int BCE = (kCK * NS + kWave * NG - 1) / (kWave * NG);
   constexpr int EB = EPI ? 2 : 1;
   constexpr int ER = EPI ? kCK : 1;
@@ -457,6 +494,7 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_bwd_kernel(BwdArgs<T> p) {
   __shared__ __attribute__((aligned(16))) float s_C[2][kCK][NS];
   __shared__ float sbuf[EPI ? 3 : 2][NG][kCK][kWave];  // per-wave partials: du, ddelta, (y)
   __shared__ float bcbuf[2][kCK][NS];                  // dB, dC wave partials
+  __shared__ float bdummy[2][kWave];                   // sink for lanes without a total
 
   const int64_t bLD = (int64_t)b * L * D;
   const int64_t bLN = (int64_t)b * L * N;
@@ -483,14 +521,14 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_bwd_kernel(BwdArgs<T> p) {
     for (int k = 0; k < RPT; ++k) {
       const int tc = min(t0 + wave + k * NG, L - 1);
       const int pr = rev ? L - 1 - tc : tc;  // output row of scan step tc
-      r_u[k] = ld(u_b + (int64_t)tc * D, dc);
-      r_dt[k] = ld(dt_b + (int64_t)tc * dtD, dd_lane);
-      r_dy[k] = ld(dy_b + (int64_t)pr * D, q);
-      if (gate) r_gz[k] = ld(z_b + (int64_t)pr * D, q);
-      if (stage_eu) r_eu[k] = ld(u_b + (int64_t)pr * D, q);
+      r_u[k] = ld32(u_b, (uint32_t)(tc * D + dc));
+      r_dt[k] = ld32(dt_b, (uint32_t)(tc * dtD + dd_lane));
+      r_dy[k] = ld32(dy_b, (uint32_t)(pr * D + q));
+      if (gate) r_gz[k] = ld32(z_b, (uint32_t)(pr * D + q));
+      if (stage_eu) r_eu[k] = ld32(u_b, (uint32_t)(pr * D + q));
       if (stage_dyo) {
-        r_dyo[k] = ld(dy_b + (int64_t)tc * D, dc);
-        if (gate) r_zo[k] = ld(z_b + (int64_t)tc * D, dc);
+        r_dyo[k] = ld32(dy_b, (uint32_t)(tc * D + dc));
+        if (gate) r_zo[k] = ld32(z_b, (uint32_t)(tc * D + dc));
       }
     }
 #pragma unroll
@@ -504,11 +542,11 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_bwd_kernel(BwdArgs<T> p) {
         gi = (t0 + i) * N + min(n, N - 1);
       }
       const int gc = min(gi, LN - 1);
-      r_B[k] = ld(B_b, gc);
-      r_C[k] = ld(C_b, gc);
+      r_B[k] = ld32(B_b, (uint32_t)gc);
+      r_C[k] = ld32(C_b, (uint32_t)gc);
     }
 #pragma unroll
-    for (int j = 0; j < NPW; ++j) r_h[j] = ck_b[((int64_t)blk * N + min(n0 + j, N - 1)) * D + dc];
+    for (int j = 0; j < NPW; ++j) r_h[j] = ld32(ck_b, (uint32_t)((blk * N + min(n0 + j, N - 1)) * D + dc));
   };
   auto commit = [&](int buf, int blk) {
     const int t0 = blk * kCK;
@@ -574,15 +612,33 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_bwd_kernel(BwdArgs<T> p) {
           dyv[i] = s_dy[buf][i][lane];
         }
       }
+      // dB / dC values of kRB consecutive steps are reduced over the wave
+      // together (8 values per wave_reduce8); the 8 lanes holding each total's
+      // first copy write it, the others write a per-lane dummy slot
+      float xb[kRB][NPW];
+      auto flush = [&](int i0, int qsel) {
+        float x8[8];
+#pragma unroll
+        for (int m = 0; m < 8; ++m) x8[m] = xb[m / NPW][m % NPW];
+        const float r = wave_reduce8(x8);
+        const int v = wave_reduce8_index(lane);
+        float* dst = (lane & 7) == 0 ? &bcbuf[qsel][i0 + v / NPW][n0 + v % NPW] : &bdummy[qsel][lane];
+        *dst = r;
+      };
       // forward recompute of the block: a_t, h_{t-1}; dC_t = sum_d dy_t h_t
 #pragma unroll
       for (int i = 0; i < kCK; ++i) {
+        if (i % kRB == 0) {
+#pragma unroll
+          for (int bi = 0; bi < kRB; ++bi)
+#pragma unroll
+            for (int j = 0; j < NPW; ++j) xb[bi][j] = 0.0f;
+        }
         if (kFull || i < tn) {
           float Bn[NPW], Cn[NPW];
           lds_vec<NPW>(&s_B[buf][i][n0], Bn);
           if (gate) lds_vec<NPW>(&s_C[buf][i][n0], Cn);
           const float w = dd[i] * uu[i];
-          float c[NPW];
           float yp = 0.0f;
 #pragma unroll
           for (int j = 0; j < NPW; ++j) {
@@ -590,25 +646,28 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_bwd_kernel(BwdArgs<T> p) {
             a_s[i][j] = a;
             hp_s[i][j] = h[j];
             h[j] = fmaf(a, h[j], Bn[j] * w);
-            c[j] = dyv[i] * h[j];
+            xb[i % kRB][j] = dyv[i] * h[j];
             if (gate) yp = fmaf(Cn[j], h[j], yp);
           }
           if (gate) sbuf[EPI ? 2 : 0][wave][i][lane] = yp;
-          const float r = wave_reduce<NPW>(c);
-          const int sr = wave_reduce_state<NPW>(lane);
-          if (sr >= 0) bcbuf[1][i][n0 + sr] = r;
         }
+        if (i % kRB == kRB - 1 && (kFull || i - (kRB - 1) < tn)) flush(i - (kRB - 1), 1);
       }
       // adjoint, backwards through the block
 #pragma unroll
       for (int i = kCK - 1; i >= 0; --i) {
+        if (i % kRB == kRB - 1) {
+#pragma unroll
+          for (int bi = 0; bi < kRB; ++bi)
+#pragma unroll
+            for (int j = 0; j < NPW; ++j) xb[bi][j] = 0.0f;
+        }
         if (kFull || i < tn) {
           float Bn[NPW], Cn[NPW];
           lds_vec<NPW>(&s_B[buf][i][n0], Bn);
           lds_vec<NPW>(&s_C[buf][i][n0], Cn);
           const float w = dd[i] * uu[i];
           float s1 = 0.0f, s2 = 0.0f;
-          float e[NPW];
 #pragma unroll
           for (int j = 0; j < NPW; ++j) {
             const float f = fmaf(Cn[j], dyv[i], g[j]);
@@ -617,15 +676,13 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_bwd_kernel(BwdArgs<T> p) {
             s2 = fmaf(Av[j], qv, s2);
             dAacc[j] = fmaf(dd[i], qv, dAacc[j]);
             s1 = fmaf(Bn[j], f, s1);
-            e[j] = f * w;
+            xb[i % kRB][j] = f * w;
             g[j] = gg;
           }
-          const float r = wave_reduce<NPW>(e);
-          const int sr = wave_reduce_state<NPW>(lane);
-          if (sr >= 0) bcbuf[0][i][n0 + sr] = r;
           sbuf[0][wave][i][lane] = dd[i] * s1;
           sbuf[1][wave][i][lane] = fmaf(uu[i], s1, s2);
         }
+        if (i % kRB == 0 && (kFull || i < tn)) flush(i, 0);
       }
     };
     if (tn == kCK) sweeps(std::true_type{}); else sweeps(std::false_type{});
@@ -755,8 +812,11 @@ int validate(const ssm_desc_t* desc, Shape* s) {
     return fail(SSM_ERR_INVALID, "batch, seqlen and dim must be >= 1");
   if (desc->dstate < 1 || desc->dstate > 32) return fail(SSM_ERR_INVALID, "dstate must be in 1..32");
   if (desc->batch > 65535) return fail(SSM_ERR_INVALID, "batch must be <= 65535");
+  // per-batch-row element offsets are 32-bit inside the kernels
   if (desc->seqlen * desc->dim > (int64_t(1) << 31) - 1 || desc->seqlen * desc->dstate > (int64_t(1) << 31) - 1)
     return fail(SSM_ERR_INVALID, "seqlen*dim must fit in int32");
+  if ((desc->seqlen / 8 + 1) * desc->dstate * desc->dim > (int64_t(1) << 31) - 1)
+    return fail(SSM_ERR_INVALID, "checkpoint rows of one batch row must fit in int32");
   if (desc->dtype != SSM_F32 && desc->dtype != SSM_BF16) return fail(SSM_ERR_INVALID, "dtype must be SSM_F32 or SSM_BF16");
   if (desc->flags & ~(SSM_REVERSE | SSM_COMPLEMENT | SSM_SKIP | SSM_GATE))
     return fail(SSM_ERR_INVALID, "unknown flag bits");
