@@ -86,6 +86,12 @@ __device__ __forceinline__ void st<bf16>(bf16* p, int64_t i, float v) {
   p[i].bits = r;
 }
 
+// store at a 32-bit unsigned offset from a (wave-uniform) base pointer
+template <typename T>
+__device__ __forceinline__ void st32(T* base, uint32_t off, float v) {
+  st(reinterpret_cast<T*>(reinterpret_cast<char*>(base) + (size_t)off * sizeof(T)), 0, v);
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ float sigmoid(float x) {
@@ -283,7 +289,10 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_fwd_kernel(FwdArgs<T> p) {
   const T* __restrict__ z_b = EPI ? p.z + bLD : nullptr;
   const T* __restrict__ B_b = p.Bc + bLN;
   const T* __restrict__ C_b = p.Cc + bLN;
+  T* __restrict__ y_b = p.y + bLD;
+  float* __restrict__ ck_b = p.ckpt != nullptr ? p.ckpt + (int64_t)b * p.nblk * N * D : nullptr;
   const int LN = L * N;
+  const int ND = N * D;
 
   // fetch() only issues loads (clamped addresses, raw values); commit(), run
   // after the tile's compute, zeroes what lies outside the tensor and writes
@@ -376,12 +385,12 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_fwd_kernel(FwdArgs<T> p) {
           __builtin_amdgcn_sched_barrier(0);
           const float* Bn = Br[i % (kPF + 1)];
           const float* Cn = Cr[i % (kPF + 1)];
-          if (p.ckpt != nullptr && (i % kCK) == 0) {
+          if (ck_b != nullptr && (i % kCK) == 0) {
             const int blk = (t0 + i) / kCK;
 #pragma unroll
             for (int j = 0; j < NPW; ++j) {
               const int n = n0 + j;
-              if (valid && n < N) p.ckpt[(((int64_t)b * p.nblk + blk) * N + n) * D + d] = h[j];
+              if (n < N && valid) st32(ck_b, (uint32_t)(blk * ND + n * D + d), h[j]);
             }
           }
           const float w = dd[i] * uu[i];
@@ -401,21 +410,27 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_fwd_kernel(FwdArgs<T> p) {
     };
     if (tn == kTT) tile(std::true_type{}); else tile(std::false_type{});
     __syncthreads();
-    for (int i = wave; i < tn; i += NG) {
-      float ys = 0.0f;
+    auto yreduce = [&](auto full_tag) {
+      constexpr bool kFull = decltype(full_tag)::value;
 #pragma unroll
-      for (int w = 0; w < NG; ++w) ys += s_y[w][i][lane];
-      if (valid) {
-        const int t = t0 + i;
-        const int pt = rev ? L - 1 - t : t;
-        if (skip) ys = fmaf(stage_eu ? s_eu[buf][i][lane] : s_u[buf][i][lane], Dq, ys);
-        if (gate) {
-          const float zz = s_ez[buf][i][lane];
-          ys *= zz * sigmoid(zz);
+      for (int k = 0; k < kTT / NG; ++k) {
+        const int i = wave + k * NG;
+        if (kFull || i < tn) {
+          float ys = 0.0f;
+#pragma unroll
+          for (int w = 0; w < NG; ++w) ys += s_y[w][i][lane];
+          const int t = t0 + i;
+          const int pt = rev ? L - 1 - t : t;
+          if (skip) ys = fmaf(stage_eu ? s_eu[buf][i][lane] : s_u[buf][i][lane], Dq, ys);
+          if (gate) {
+            const float zz = s_ez[buf][i][lane];
+            ys *= zz * sigmoid(zz);
+          }
+          if (valid) st32(y_b, (uint32_t)(pt * D + q), ys);
         }
-        st(p.y, bLD + (int64_t)pt * D + q, ys);
       }
-    }
+    };
+    if (tn == kTT) yreduce(std::true_type{}); else yreduce(std::false_type{});
     if (more) commit(buf ^ 1, t0 + kTT);
     __syncthreads();
   }
@@ -509,6 +524,9 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_bwd_kernel(BwdArgs<T> p) {
   const T* __restrict__ B_b = p.Bc + bLN;
   const T* __restrict__ C_b = p.Cc + bLN;
   const float* __restrict__ ck_b = p.ckpt + (int64_t)b * p.nblk * N * D;
+  T* __restrict__ du_b = p.du + bLD;
+  T* __restrict__ ddt_b = p.ddelta + bLD;  // only used when delta is (B,L,D)
+  T* __restrict__ dz_b = EPI ? p.dz + bLD : nullptr;
   const int LN = L * N;
 
   // fetch() only issues loads; commit() (after the block's compute) masks,
@@ -689,40 +707,48 @@ __global__ void __launch_bounds__(kWave* NG, 1) ssm_bwd_kernel(BwdArgs<T> p) {
     __syncthreads();
 
     // combine the per-wave partials; write du, ddelta (and dz)
-    for (int i = wave; i < tn; i += NG) {
-      float du = 0.0f, ddt = 0.0f;
+    auto combine = [&](auto full_tag) {
+      constexpr bool kFull = decltype(full_tag)::value;
 #pragma unroll
-      for (int w = 0; w < NG; ++w) {
-        du += sbuf[0][w][i][lane];
-        ddt += sbuf[1][w][i][lane];
-      }
-      const int t = t0 + i;
-      const float uu = s_u[buf][i][lane];
-      if (skip) {
-        // y_out[t,d] holds u[t,d]*D[d] (selectssm.py:238): its gradient lands on u[t,d]
-        const float dyo = stage_dyo ? s_dyo[buf][i][lane] : s_dy[buf][i][lane];
-        du = fmaf(Dd, dyo, du);
-        dDacc = fmaf(dyo, uu, dDacc);
-      }
-      if (valid) {
-        st(p.du, bLD + (int64_t)t * D + dc, du);
-        if (p.dstride) st(p.ddelta, bLDt + (int64_t)t * dtD + dc, ddt);
-      }
-      if (!p.dstride) {
-        const float tot = wave_sum(valid ? ddt : 0.0f);
-        if (lane == 0) p.ws_ddt[((int64_t)cb * p.Bt + b) * L + t] = tot;
-      }
-      if (gate && valid) {
-        float ys = 0.0f;
+      for (int k = 0; k < kCK / NG; ++k) {
+        const int i = wave + k * NG;
+        if (kFull || i < tn) {
+          float du = 0.0f, ddt = 0.0f;
 #pragma unroll
-        for (int w = 0; w < NG; ++w) ys += sbuf[EPI ? 2 : 0][w][i][lane];
-        if (skip) ys = fmaf(stage_eu ? s_eu[buf][i][lane] : uu, Dq, ys);
-        const float zz = s_gz[buf][i][lane];
-        const float sg = sigmoid(zz);
-        const int pt = rev ? L - 1 - t : t;
-        st(p.dz, bLD + (int64_t)pt * D + q, s_go[buf][i][lane] * ys * sg * (1.0f + zz * (1.0f - sg)));
+          for (int w = 0; w < NG; ++w) {
+            du += sbuf[0][w][i][lane];
+            ddt += sbuf[1][w][i][lane];
+          }
+          const int t = t0 + i;
+          const float uu = s_u[buf][i][lane];
+          if (skip) {
+            // y_out[t,d] holds u[t,d]*D[d] (selectssm.py:238): its gradient lands on u[t,d]
+            const float dyo = stage_dyo ? s_dyo[buf][i][lane] : s_dy[buf][i][lane];
+            du = fmaf(Dd, dyo, du);
+            dDacc = fmaf(dyo, uu, dDacc);
+          }
+          if (valid) {
+            st32(du_b, (uint32_t)(t * D + dc), du);
+            if (p.dstride) st32(ddt_b, (uint32_t)(t * D + dc), ddt);
+          }
+          if (!p.dstride) {
+            const float tot = wave_sum(valid ? ddt : 0.0f);
+            if (lane == 0) p.ws_ddt[((int64_t)cb * p.Bt + b) * L + t] = tot;
+          }
+          if (gate && valid) {
+            float ys = 0.0f;
+#pragma unroll
+            for (int w = 0; w < NG; ++w) ys += sbuf[EPI ? 2 : 0][w][i][lane];
+            if (skip) ys = fmaf(stage_eu ? s_eu[buf][i][lane] : uu, Dq, ys);
+            const float zz = s_gz[buf][i][lane];
+            const float sg = sigmoid(zz);
+            const int pt = rev ? L - 1 - t : t;
+            st32(dz_b, (uint32_t)(pt * D + q), s_go[buf][i][lane] * ys * sg * (1.0f + zz * (1.0f - sg)));
+          }
+        }
       }
-    }
+    };
+    if (tn == kCK) combine(std::true_type{}); else combine(std::false_type{});
     // dB, dC partials of this channel block, coalesced
     {
       float* __restrict__ wB = p.ws_dB + (((int64_t)cb * p.Bt + b) * L + t0) * N;
