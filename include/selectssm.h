@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define SSM_ABI_VERSION 1
+#define SSM_ABI_VERSION 2
 
 /* error codes */
 #define SSM_OK 0
@@ -55,7 +55,10 @@ typedef struct ssm_desc {
   int32_t dtype;          /* SSM_F32 or SSM_BF16 for u, delta, Bc, Cc, z, y, dy, du, ddelta, dB, dC, dz */
   uint32_t flags;         /* SSM_REVERSE | SSM_COMPLEMENT | SSM_SKIP | SSM_GATE */
   int32_t delta_broadcast;/* 1: delta is (B,L,1) and shared by all channels */
-  int32_t reserved;       /* must be 0 */
+  int32_t segments;       /* time segments per row: 0 = chosen from the shape, else 1..1024
+                             (a row's time axis is split into this many segments that run
+                             in parallel, joined by their carries; results agree with 1
+                             segment up to fp32 rounding) */
 } ssm_desc_t;
 
 /* Version of this ABI (SSM_ABI_VERSION). */
@@ -68,8 +71,13 @@ const char* ssm_last_error(void);
  * the scan's time axis), needed by ssm_bwd.  Returns 0 for an invalid desc. */
 size_t ssm_ckpt_bytes(const ssm_desc_t* desc);
 
+/* Bytes of scratch `workspace` that ssm_fwd needs (per-segment carries of a
+ * time-split scan).  0 when the desc runs as one segment per row (workspace
+ * may then be NULL) and for an invalid desc (ssm_last_error() tells which). */
+size_t ssm_fwd_workspace_bytes(const ssm_desc_t* desc);
+
 /* Bytes of scratch `workspace` that ssm_bwd needs (partial sums for dB, dC,
- * dA, dD).  Returns 0 for an invalid desc. */
+ * dA, dD; per-segment adjoint carries).  Returns 0 for an invalid desc. */
 size_t ssm_bwd_workspace_bytes(const ssm_desc_t* desc);
 
 /*
@@ -82,12 +90,13 @@ size_t ssm_bwd_workspace_bytes(const ssm_desc_t* desc);
  *   y[b,p,q] = (scan(u,delta,A,Bc,Cc)[b,t,d] + skip) * gate
  * with (p,q) = (t,d) or the reverse / complement map.
  * Dskip is required iff SSM_SKIP, z iff SSM_GATE.  ckpt (ssm_ckpt_bytes) may
- * be NULL for inference; ssm_bwd needs it.
+ * be NULL for inference; ssm_bwd needs it.  workspace has
+ * ssm_fwd_workspace_bytes (NULL allowed when that is 0).
  */
 int ssm_fwd(void* stream, const ssm_desc_t* desc,
             const void* u, const void* delta, const float* A,
             const void* Bc, const void* Cc, const float* Dskip, const void* z,
-            void* y, float* ckpt);
+            void* y, float* ckpt, void* workspace);
 
 /*
  * Backward of ssm_fwd for upstream gradient dy (same layout as y).

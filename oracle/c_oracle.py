@@ -27,42 +27,49 @@ def lib():
         if not os.path.exists(LIB):
             build()
         h = ctypes.CDLL(LIB)
-        fp = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
         i = ctypes.c_int
-        h.oracle_scan_fwd.restype = i
-        h.oracle_scan_fwd.argtypes = [i, i, i, i, fp, fp, fp, fp, fp, fp, i, i, i]
-        h.oracle_scan_bwd.restype = i
-        h.oracle_scan_bwd.argtypes = [i, i, i, i, fp, fp, fp, fp, fp, fp, fp, fp, fp, fp, fp, i, i, i]
+        for sfx, dt in (("", np.float32), ("_f64", np.float64)):
+            fp = np.ctypeslib.ndpointer(dtype=dt, flags="C_CONTIGUOUS")
+            f = getattr(h, "oracle_scan_fwd" + sfx)
+            f.restype = i
+            f.argtypes = [i, i, i, i, fp, fp, fp, fp, fp, fp, i, i, i]
+            g = getattr(h, "oracle_scan_bwd" + sfx)
+            g.restype = i
+            g.argtypes = [i, i, i, i, fp, fp, fp, fp, fp, fp, fp, fp, fp, fp, fp, i, i, i]
         _lib = h
     return _lib
 
 
-def _f32(x):
-    return np.ascontiguousarray(x, dtype=np.float32)
+_PREC = {"f32": ("", np.float32), "f64": ("_f64", np.float64)}
 
 
-def scan_fwd(u, dt, A, B, C, min_recursion_length=2, recursive_split=2, nthreads=0):
-    u, dt, A, B, C = map(_f32, (u, dt, A, B, C))
+def scan_fwd(u, dt, A, B, C, min_recursion_length=2, recursive_split=2, nthreads=0, precision="f32"):
+    """y of the reference's recursive custom-VJP forward, in float32 or float64."""
+    sfx, dtype = _PREC[precision]
+    u, dt, A, B, C = (np.ascontiguousarray(x, dtype=dtype) for x in (u, dt, A, B, C))
     Bt, L, D = u.shape
     N = A.shape[1]
-    y = np.empty((Bt, L, D), np.float32)
-    rc = lib().oracle_scan_fwd(Bt, L, D, N, u, dt, A, B, C, y, min_recursion_length, recursive_split, nthreads)
+    y = np.empty((Bt, L, D), dtype)
+    rc = getattr(lib(), "oracle_scan_fwd" + sfx)(Bt, L, D, N, u, dt, A, B, C, y, min_recursion_length,
+                                                 recursive_split, nthreads)
     if rc:
         raise ValueError("oracle_scan_fwd rejected the arguments")
     return y
 
 
-def scan_bwd(u, dt, A, B, C, dy, min_recursion_length=2, recursive_split=2, nthreads=0):
-    u, dt, A, B, C, dy = map(_f32, (u, dt, A, B, C, dy))
+def scan_bwd(u, dt, A, B, C, dy, min_recursion_length=2, recursive_split=2, nthreads=0, precision="f32"):
+    """(du, ddt, dA, dB, dC) of the reference's custom-VJP backward, in float32 or float64."""
+    sfx, dtype = _PREC[precision]
+    u, dt, A, B, C, dy = (np.ascontiguousarray(x, dtype=dtype) for x in (u, dt, A, B, C, dy))
     Bt, L, D = u.shape
     N = A.shape[1]
-    du = np.empty((Bt, L, D), np.float32)
-    ddt = np.empty((Bt, L, D), np.float32)
-    dA = np.empty((D, N), np.float32)
-    dB = np.empty((Bt, L, N), np.float32)
-    dC = np.empty((Bt, L, N), np.float32)
-    rc = lib().oracle_scan_bwd(Bt, L, D, N, u, dt, A, B, C, dy, du, ddt, dA, dB, dC, min_recursion_length,
-                               recursive_split, nthreads)
+    du = np.empty((Bt, L, D), dtype)
+    ddt = np.empty((Bt, L, D), dtype)
+    dA = np.empty((D, N), dtype)
+    dB = np.empty((Bt, L, N), dtype)
+    dC = np.empty((Bt, L, N), dtype)
+    rc = getattr(lib(), "oracle_scan_bwd" + sfx)(Bt, L, D, N, u, dt, A, B, C, dy, du, ddt, dA, dB, dC,
+                                                 min_recursion_length, recursive_split, nthreads)
     if rc:
         raise ValueError("oracle_scan_bwd rejected the arguments")
     return du, ddt, dA, dB, dC

@@ -21,8 +21,12 @@
  *             f_t, then the closed forms of 154-160.
  * Rows are independent except for the sums over channels (dB, dC) and over
  * (batch, time) (dA); those are accumulated per thread and summed at the end.
- * OpenMP parallelises over rows.  All arithmetic is float32 like the
+ * OpenMP parallelises over rows.  The arithmetic is float32 like the
  * reference; the associative-scan leaf keeps the reference's combine order.
+ * Compiled a second time with -DORACLE_F64, the same algorithm runs in
+ * float64 and exports its entry points with an _f64 suffix: an fp64 oracle
+ * for sizes the numpy restatement cannot reach (long sums such as dA over
+ * 2^20 steps).
  */
 #include <math.h>
 #include <stdint.h>
@@ -32,29 +36,39 @@
 #include <omp.h>
 #endif
 
+#ifdef ORACLE_F64
+typedef double real;
+#define EXP exp
+#define SUFFIX(name) name##_f64
+#else
+typedef float real;
+#define EXP expf
+#define SUFFIX(name) name
+#endif
+
 #define MAXN 64
 
 typedef struct {
   int L, N, min_len, split;
-  const float *u, *dt, *Bc, *Cc, *dy; /* row views: u[t*ustride] etc. */
+  const real *u, *dt, *Bc, *Cc, *dy; /* row views: u[t*ustride] etc. */
   int64_t ustride, bstride;           /* D for (B,L,D) rows, N for (B,L,N) rows */
-  const float* A;                     /* A[d, 0..N) */
-  float* y;                           /* forward output row */
-  float *du, *ddt;                    /* backward output rows */
-  float *dB, *dC;                     /* (L,N) thread-private accumulators */
-  float* dA;                          /* (N) thread-private accumulator */
-  float* scratch;                     /* leaf workspace */
+  const real* A;                     /* A[d, 0..N) */
+  real* y;                           /* forward output row */
+  real *du, *ddt;                    /* backward output rows */
+  real *dB, *dC;                     /* (L,N) thread-private accumulators */
+  real* dA;                          /* (N) thread-private accumulator */
+  real* scratch;                     /* leaf workspace */
 } Row;
 
 /* inclusive scan of (g,h) pairs with the odd/even recursion of
  * jax.lax.associative_scan; combine(l, r) = (g_l g_r, g_r h_l + h_r). */
-static void assoc_scan(float* g, float* h, int n, float* tmp) {
+static void assoc_scan(real* g, real* h, int n, real* tmp) {
   if (n < 2) return;
   int m = n / 2; /* number of pairs */
-  float* rg = tmp;
-  float* rh = tmp + m;
+  real* rg = tmp;
+  real* rh = tmp + m;
   for (int i = 0; i < m; ++i) {
-    float gl = g[2 * i], hl = h[2 * i], gr = g[2 * i + 1], hr = h[2 * i + 1];
+    real gl = g[2 * i], hl = h[2 * i], gr = g[2 * i + 1], hr = h[2 * i + 1];
     rg[i] = gl * gr;
     rh[i] = gr * hl + hr;
   }
@@ -62,7 +76,7 @@ static void assoc_scan(float* g, float* h, int n, float* tmp) {
   /* odd positions 1,3,.. take the reduced prefixes; even positions 2,4,.. combine
    * the previous odd prefix with the original element */
   for (int i = 1; 2 * i < n; ++i) {
-    float gl = rg[i - 1], hl = rh[i - 1], gr = g[2 * i], hr = h[2 * i];
+    real gl = rg[i - 1], hl = rh[i - 1], gr = g[2 * i], hr = h[2 * i];
     g[2 * i] = gl * gr;
     h[2 * i] = gr * hl + hr;
   }
@@ -74,7 +88,7 @@ static void assoc_scan(float* g, float* h, int n, float* tmp) {
 
 /* ---------------------------------------------------------------- forward */
 
-static void fwd_rec(Row* r, int t0, int len, float* g, float* h) {
+static void fwd_rec(Row* r, int t0, int len, real* g, real* h) {
   if (len > r->min_len && len % r->split == 0) {
     int m = len / r->split;
     for (int i = 0; i < r->split; ++i) fwd_rec(r, t0 + i * m, m, g, h);
@@ -82,19 +96,19 @@ static void fwd_rec(Row* r, int t0, int len, float* g, float* h) {
   }
   const int N = r->N;
   for (int n = 0; n < N; ++n) {
-    float* ga = r->scratch;
-    float* ha = ga + len;
-    float* tmp = ha + len;
+    real* ga = r->scratch;
+    real* ha = ga + len;
+    real* tmp = ha + len;
     for (int i = 0; i < len; ++i) {
       const int t = t0 + i;
-      const float d = r->dt[t * r->ustride];
-      ga[i] = expf(r->A[n] * d);
+      const real d = r->dt[t * r->ustride];
+      ga[i] = EXP(r->A[n] * d);
       ha[i] = r->Bc[t * r->bstride + n] * r->u[t * r->ustride] * d;
     }
     assoc_scan(ga, ha, len, tmp);
     for (int i = 0; i < len; ++i) {
       const int t = t0 + i;
-      const float hs = ga[i] * h[n] + ha[i];
+      const real hs = ga[i] * h[n] + ha[i];
       r->y[t * r->ustride] += r->Cc[t * r->bstride + n] * hs;
       if (i == len - 1) {
         g[n] = ga[i] * g[n];
@@ -106,21 +120,21 @@ static void fwd_rec(Row* r, int t0, int len, float* g, float* h) {
 
 /* --------------------------------------------------------------- backward */
 
-static void bwd_rec(Row* r, int t0, int len, float* h_left, const float* fa_right) {
+static void bwd_rec(Row* r, int t0, int len, real* h_left, const real* fa_right) {
   const int N = r->N;
   if (len > r->min_len && len % r->split == 0) {
     const int m = len / r->split;
-    float* fas = (float*)malloc(sizeof(float) * r->split * N);
-    float fa[MAXN];
-    memcpy(fa, fa_right, sizeof(float) * N);
+    real* fas = (real*)malloc(sizeof(real) * r->split * N);
+    real fa[MAXN];
+    memcpy(fa, fa_right, sizeof(real) * N);
     for (int i = r->split - 1; i >= 0; --i) {
-      memcpy(fas + i * N, fa, sizeof(float) * N);
+      memcpy(fas + i * N, fa, sizeof(real) * N);
       for (int t = t0 + i * m + m - 1; t >= t0 + i * m; --t) {
-        const float d = r->dt[t * r->ustride];
-        const float dyv = r->dy[t * r->ustride];
+        const real d = r->dt[t * r->ustride];
+        const real dyv = r->dy[t * r->ustride];
         for (int n = 0; n < N; ++n) {
-          const float alpha = expf(r->A[n] * d);
-          const float f = fa[n] + r->Cc[t * r->bstride + n] * dyv;
+          const real alpha = EXP(r->A[n] * d);
+          const real f = fa[n] + r->Cc[t * r->bstride + n] * dyv;
           fa[n] = f * alpha;
         }
       }
@@ -129,40 +143,40 @@ static void bwd_rec(Row* r, int t0, int len, float* h_left, const float* fa_righ
     free(fas);
     return;
   }
-  float* hs = r->scratch;   /* len*N: h_{t-1} */
-  float* al = hs + len * N; /* len*N: alpha_t */
-  float* fs = al + len * N; /* len*N: f_t */
+  real* hs = r->scratch;   /* len*N: h_{t-1} */
+  real* al = hs + len * N; /* len*N: alpha_t */
+  real* fs = al + len * N; /* len*N: f_t */
   for (int i = 0; i < len; ++i) {
     const int t = t0 + i;
-    const float d = r->dt[t * r->ustride], uu = r->u[t * r->ustride];
+    const real d = r->dt[t * r->ustride], uu = r->u[t * r->ustride];
     for (int n = 0; n < N; ++n) {
-      const float a = expf(r->A[n] * d);
+      const real a = EXP(r->A[n] * d);
       al[i * N + n] = a;
       hs[i * N + n] = h_left[n];
       h_left[n] = h_left[n] * a + r->Bc[t * r->bstride + n] * uu * d;
     }
   }
-  float fa[MAXN];
-  memcpy(fa, fa_right, sizeof(float) * N);
+  real fa[MAXN];
+  memcpy(fa, fa_right, sizeof(real) * N);
   for (int i = len - 1; i >= 0; --i) {
     const int t = t0 + i;
-    const float dyv = r->dy[t * r->ustride];
+    const real dyv = r->dy[t * r->ustride];
     for (int n = 0; n < N; ++n) {
-      const float f = fa[n] + r->Cc[t * r->bstride + n] * dyv;
+      const real f = fa[n] + r->Cc[t * r->bstride + n] * dyv;
       fs[i * N + n] = f;
       fa[n] = f * al[i * N + n];
     }
   }
   for (int i = 0; i < len; ++i) {
     const int t = t0 + i;
-    const float d = r->dt[t * r->ustride], uu = r->u[t * r->ustride], dyv = r->dy[t * r->ustride];
-    float dx = 0.0f, ddt = 0.0f;
+    const real d = r->dt[t * r->ustride], uu = r->u[t * r->ustride], dyv = r->dy[t * r->ustride];
+    real dx = (real)0, ddt = (real)0;
     for (int n = 0; n < N; ++n) {
-      const float f = fs[i * N + n];
-      const float Bn = r->Bc[t * r->bstride + n];
-      const float ah = al[i * N + n] * hs[i * N + n];
-      const float df = d * f;
-      const float hnext = (i + 1 < len) ? hs[(i + 1) * N + n] : h_left[n];
+      const real f = fs[i * N + n];
+      const real Bn = r->Bc[t * r->bstride + n];
+      const real ah = al[i * N + n] * hs[i * N + n];
+      const real df = d * f;
+      const real hnext = (i + 1 < len) ? hs[(i + 1) * N + n] : h_left[n];
       dx += df * Bn;
       r->dA[n] += df * ah;
       r->dB[t * N + n] += df * uu;
@@ -187,17 +201,17 @@ static size_t leaf_scratch_floats(int L, int N, int min_len, int split) {
  * Forward: y (B,L,D) from u, dt (B,L,D), A (D,N), Bc, Cc (B,L,N).
  * Returns 0, or -1 when N > 64 or recursive_split < 2.
  */
-int oracle_scan_fwd(int B, int L, int D, int N, const float* u, const float* dt, const float* A, const float* Bc,
-                    const float* Cc, float* y, int min_len, int split, int nthreads) {
+int SUFFIX(oracle_scan_fwd)(int B, int L, int D, int N, const real* u, const real* dt, const real* A, const real* Bc,
+                    const real* Cc, real* y, int min_len, int split, int nthreads) {
   if (N > MAXN || split < 2) return -1;
 #ifdef _OPENMP
   if (nthreads > 0) omp_set_num_threads(nthreads);
 #endif
   const size_t sf = leaf_scratch_floats(L, N, min_len, split);
-  memset(y, 0, sizeof(float) * (size_t)B * L * D);
+  memset(y, 0, sizeof(real) * (size_t)B * L * D);
 #pragma omp parallel
   {
-    float* scratch = (float*)malloc(sizeof(float) * sf);
+    real* scratch = (real*)malloc(sizeof(real) * sf);
 #pragma omp for schedule(dynamic, 4)
     for (int64_t row = 0; row < (int64_t)B * D; ++row) {
       const int b = (int)(row / D), d = (int)(row % D);
@@ -216,10 +230,10 @@ int oracle_scan_fwd(int B, int L, int D, int N, const float* u, const float* dt,
       r.A = A + (int64_t)d * N;
       r.y = y + (int64_t)b * L * D + d;
       r.scratch = scratch;
-      float g[MAXN], h[MAXN];
+      real g[MAXN], h[MAXN];
       for (int n = 0; n < N; ++n) {
-        g[n] = 1.0f;
-        h[n] = 0.0f;
+        g[n] = (real)1;
+        h[n] = (real)0;
       }
       fwd_rec(&r, 0, L, g, h);
     }
@@ -229,40 +243,40 @@ int oracle_scan_fwd(int B, int L, int D, int N, const float* u, const float* dt,
 }
 
 /* add one thread's channel sums for batch row b into dB, dC and clear them */
-static void flush_bc(float* dB, float* dC, float* pB, float* pC, int b, int L, int N) {
+static void flush_bc(real* dB, real* dC, real* pB, real* pC, int b, int L, int N) {
 #pragma omp critical
   {
-    float* oB = dB + (int64_t)b * L * N;
-    float* oC = dC + (int64_t)b * L * N;
+    real* oB = dB + (int64_t)b * L * N;
+    real* oC = dC + (int64_t)b * L * N;
     for (int64_t i = 0; i < (int64_t)L * N; ++i) {
       oB[i] += pB[i];
       oC[i] += pC[i];
     }
   }
-  memset(pB, 0, sizeof(float) * (size_t)L * N);
-  memset(pC, 0, sizeof(float) * (size_t)L * N);
+  memset(pB, 0, sizeof(real) * (size_t)L * N);
+  memset(pC, 0, sizeof(real) * (size_t)L * N);
 }
 
 /*
  * Backward (custom VJP): du, ddt (B,L,D), dA (D,N), dB, dC (B,L,N) for dy.
  */
-int oracle_scan_bwd(int B, int L, int D, int N, const float* u, const float* dt, const float* A, const float* Bc,
-                    const float* Cc, const float* dy, float* du, float* ddt, float* dA, float* dB, float* dC,
+int SUFFIX(oracle_scan_bwd)(int B, int L, int D, int N, const real* u, const real* dt, const real* A, const real* Bc,
+                    const real* Cc, const real* dy, real* du, real* ddt, real* dA, real* dB, real* dC,
                     int min_len, int split, int nthreads) {
   if (N > MAXN || split < 2) return -1;
 #ifdef _OPENMP
   if (nthreads > 0) omp_set_num_threads(nthreads);
 #endif
   const size_t sf = leaf_scratch_floats(L, N, min_len, split);
-  memset(dA, 0, sizeof(float) * (size_t)D * N);
-  memset(dB, 0, sizeof(float) * (size_t)B * L * N);
-  memset(dC, 0, sizeof(float) * (size_t)B * L * N);
+  memset(dA, 0, sizeof(real) * (size_t)D * N);
+  memset(dB, 0, sizeof(real) * (size_t)B * L * N);
+  memset(dC, 0, sizeof(real) * (size_t)B * L * N);
 #pragma omp parallel
   {
-    float* scratch = (float*)malloc(sizeof(float) * sf);
-    float* pB = (float*)calloc((size_t)L * N, sizeof(float));
-    float* pC = (float*)calloc((size_t)L * N, sizeof(float));
-    float* pA = (float*)calloc((size_t)D * N, sizeof(float));
+    real* scratch = (real*)malloc(sizeof(real) * sf);
+    real* pB = (real*)calloc((size_t)L * N, sizeof(real));
+    real* pC = (real*)calloc((size_t)L * N, sizeof(real));
+    real* pA = (real*)calloc((size_t)D * N, sizeof(real));
     int cur_b = -1;
 #pragma omp for schedule(static)
     for (int64_t row = 0; row < (int64_t)B * D; ++row) {
@@ -291,7 +305,7 @@ int oracle_scan_bwd(int B, int L, int D, int N, const float* u, const float* dt,
       r.dC = pC;
       r.dA = pA + (int64_t)d * N;
       r.scratch = scratch;
-      float h[MAXN] = {0}, fa[MAXN] = {0};
+      real h[MAXN] = {0}, fa[MAXN] = {0};
       bwd_rec(&r, 0, L, h, fa);
     }
     if (cur_b >= 0) flush_bc(dB, dC, pB, pC, cur_b, L, N);

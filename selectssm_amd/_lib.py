@@ -23,13 +23,14 @@ SSM_COMPLEMENT = 2
 SSM_SKIP = 4
 SSM_GATE = 8
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # every symbol include/selectssm.h declares
 EXPORTS = (
     "ssm_abi_version",
     "ssm_last_error",
     "ssm_ckpt_bytes",
+    "ssm_fwd_workspace_bytes",
     "ssm_bwd_workspace_bytes",
     "ssm_fwd",
     "ssm_bwd",
@@ -47,7 +48,7 @@ class SsmDesc(ctypes.Structure):
         ("dtype", ctypes.c_int32),
         ("flags", ctypes.c_uint32),
         ("delta_broadcast", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("segments", ctypes.c_int32),
     ]
 
 
@@ -72,10 +73,12 @@ def _declare(lib):
     lib.ssm_last_error.argtypes = []
     lib.ssm_ckpt_bytes.restype = ctypes.c_size_t
     lib.ssm_ckpt_bytes.argtypes = [dp]
+    lib.ssm_fwd_workspace_bytes.restype = ctypes.c_size_t
+    lib.ssm_fwd_workspace_bytes.argtypes = [dp]
     lib.ssm_bwd_workspace_bytes.restype = ctypes.c_size_t
     lib.ssm_bwd_workspace_bytes.argtypes = [dp]
     lib.ssm_fwd.restype = ctypes.c_int
-    lib.ssm_fwd.argtypes = [vp, dp, vp, vp, fp, vp, vp, fp, vp, vp, fp]
+    lib.ssm_fwd.argtypes = [vp, dp, vp, vp, fp, vp, vp, fp, vp, vp, fp, vp]
     lib.ssm_bwd.restype = ctypes.c_int
     lib.ssm_bwd.argtypes = [vp, dp, vp, vp, fp, vp, vp, fp, vp, fp, vp, vp, vp, fp, vp, vp, fp, vp, vp]
 
@@ -102,6 +105,16 @@ def check(code: int) -> None:
         raise SsmError(code, lib().ssm_last_error().decode())
 
 
-def make_desc(batch, seqlen, dim, dstate, dtype=SSM_F32, flags=0, delta_broadcast=False) -> SsmDesc:
+def make_desc(batch, seqlen, dim, dstate, dtype=SSM_F32, flags=0, delta_broadcast=False, segments=0) -> SsmDesc:
     return SsmDesc(int(batch), int(seqlen), int(dim), int(dstate), int(dtype), int(flags),
-                   1 if delta_broadcast else 0, 0)
+                   1 if delta_broadcast else 0, int(segments))
+
+
+def size_query(fn, desc, allow_zero=False) -> int:
+    """Call a ``ssm_*_bytes`` query; a 0 with an error message set is an invalid desc."""
+    n = fn(ctypes.byref(desc))
+    if n == 0:
+        msg = lib().ssm_last_error().decode()
+        if msg or not allow_zero:
+            raise SsmError(SSM_ERR_INVALID, msg or "size query returned 0")
+    return n

@@ -1,10 +1,16 @@
 // selectssm.hip — selective-scan forward/backward for MI355X (gfx950, CDNA4).
 //
 // Work decomposition (both kernels)
-//   * workgroup = (block of 32 channels, batch row); time runs sequentially
-//     inside the workgroup, so no carry crosses workgroups.  With 32 channels
-//     per workgroup the grid has 2x as many workgroups as 64-channel blocks,
-//     and a CU holds two of them whose barriers are independent.
+//   * workgroup = (block of 32 channels, batch row, time segment); time runs
+//     sequentially inside the workgroup.  With 32 channels per workgroup a CU
+//     holds two workgroups whose barriers are independent.
+//   * rows too few to fill the chip (B * ceil(D/32) small: long-sequence
+//     shapes) are split in time into segments joined by carries: an aggregate
+//     pass gives each segment's (sum of delta, end state from a zero start),
+//     and each segment of the main pass folds the earlier segments' aggregates
+//     into its starting state (the combine of selectssm.py:81-85 applied to
+//     whole segments).  The backward does the same for the adjoint carry,
+//     right to left.
 //   * lane = channel: lane l holds channel l & 31, and the two 32-lane halves
 //     of a wave hold different states of the same 32 channels.  Each lane keeps
 //     2 states, a wave 4, and the NG = ceil(N/4) waves of a workgroup all N.
@@ -28,6 +34,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <algorithm>
 #include <cstdio>
 #include <string>
 #include <type_traits>
@@ -190,15 +197,26 @@ struct FwdArgs {
   const T* z;
   T* y;
   float* ckpt;
+  float* agg_H;  // [B][nseg][N][D]: state at the end of each segment from a zero start
+  float* agg_S;  // [B][nseg][D]: sum of delta over each segment
   int L, D, N, nblk;
-  int dstride;  // 1, or 0 for a (B,L,1) delta
+  int seg_len, nseg;  // time segments per row (seg_len a multiple of kTT)
+  int dstride;        // 1, or 0 for a (B,L,1) delta
   uint32_t flags;
 };
 
 // NG waves (4 states each) per workgroup; EPI: the skip / gate epilogue is
-// fused (its extra staging only exists in EPI builds).
-template <int NG, bool EPI, typename T>
+// fused (its extra staging only exists in EPI builds).  Workgroup
+// (cb, b, seg) scans time segment seg of its rows.
+//   AGG = false: the segment starts from the state the earlier segments hand
+//     over (folded from their aggregates) and writes y and the checkpoints.
+//   AGG = true: aggregate pass for a time-split scan: the segment's state at
+//     its end from a zero start, and its sum of delta, so that
+//     h_end = exp(A * sum delta) * h_start + H (the combine of
+//     selectssm.py:81-85 applied to a whole segment).
+template <int NG, bool EPI, bool AGG, typename T>
 __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kernel(FwdArgs<T> p) {
+  static_assert(!(EPI && AGG), "the aggregate pass has no epilogue");
   constexpr int NS = NG * kSPW;         // padded state count
   constexpr int NT = kWave * NG;        // threads
   constexpr int RPT = kTT * kCh / NT;   // staged (step, channel) elements per thread
@@ -215,7 +233,10 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kerne
   const int hf = lane >> 5;
   const int b = blockIdx.y;
   const int cb = blockIdx.x;
+  const int seg = blockIdx.z;
   const int L = p.L, D = p.D, N = p.N;
+  const int t_lo = seg * p.seg_len;
+  const int t_hi = min(L, t_lo + p.seg_len);
   const int d = cb * kCh + c;
   const bool valid = d < D;
   const int dc = valid ? d : 0;
@@ -242,12 +263,33 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kerne
     A2[j] = (valid && n < N) ? p.A[(int64_t)dc * N + n] * kLog2e : 0.0f;
     h[j] = 0.0f;
   }
+  if (!AGG && seg > 0) {
+    // state entering this segment: fold the earlier segments' aggregates in order
+    const float* __restrict__ aS = p.agg_S + (int64_t)b * p.nseg * D + dc;
+    const float* __restrict__ aH = p.agg_H + (int64_t)b * p.nseg * N * D + dc;
+    const int nc0 = min(n0, N - 1), nc1 = min(n0 + 1, N - 1);
+#pragma unroll 4
+    for (int s = 0; s < seg; ++s) {
+      const float sd = aS[(int64_t)s * D];
+      const float H0 = aH[((int64_t)s * N + nc0) * D];
+      const float H1 = aH[((int64_t)s * N + nc1) * D];
+      h[0] = fmaf(fast_exp2(A2[0] * sd), h[0], H0);
+      h[1] = fmaf(fast_exp2(A2[1] * sd), h[1], H1);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      if (!(valid && n0 + j < N)) h[j] = 0.0f;
+  }
+  float dsum = 0.0f;  // AGG: sum of delta over the segment (channel c)
 
+  constexpr int CB = AGG ? 1 : 2;    // the aggregate pass does not stage C
+  constexpr int CR = AGG ? 1 : kTT;
+  constexpr int YG = AGG ? 1 : NG;   // nor y
   __shared__ float s_u[2][kTT][kCh], s_dt[2][kTT][kCh];
   __shared__ float s_eu[EB][ER][kCh], s_ez[EB][ER][kCh];
   __shared__ __attribute__((aligned(16))) float s_B[2][kTT][NS];
-  __shared__ __attribute__((aligned(16))) float s_C[2][kTT][NS];
-  __shared__ float s_y[NG][kTT][kCh];
+  __shared__ __attribute__((aligned(16))) float s_C[CB][CR][NS];
+  __shared__ float s_y[YG][CR][kCh];
 
   const int64_t bLD = (int64_t)b * L * D;
   const int64_t bLN = (int64_t)b * L * N;
@@ -292,7 +334,7 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kerne
       }
       const int gc = min(gi, LN - 1);
       r_B[k] = ld32(B_b, (uint32_t)gc);
-      r_C[k] = ld32(C_b, (uint32_t)gc);
+      if (!AGG) r_C[k] = ld32(C_b, (uint32_t)gc);
     }
   };
   auto commit = [&](int buf, int t0) {
@@ -311,16 +353,18 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kerne
       const int i = e / NS, n = e - (e / NS) * NS;
       const bool in = t0 + i < L && n < N;
       (&s_B[buf][0][0])[e] = in ? r_B[k] : 0.0f;
-      (&s_C[buf][0][0])[e] = in ? r_C[k] : 0.0f;
+      if (!AGG) (&s_C[buf][0][0])[e] = in ? r_C[k] : 0.0f;
     }
   };
 
-  fetch(0);
-  commit(0, 0);
+  // segments start on tile boundaries (seg_len is a multiple of kTT), so
+  // only the tile at L can be partial
+  fetch(t_lo);
+  commit(0, t_lo);
   __syncthreads();
   int buf = 0;
-  for (int t0 = 0; t0 < L; t0 += kTT, buf ^= 1) {
-    const bool more = t0 + kTT < L;
+  for (int t0 = t_lo; t0 < t_hi; t0 += kTT, buf ^= 1) {
+    const bool more = t0 + kTT < t_hi;
     if (more) fetch(t0 + kTT);
     const int tn = min(kTT, L - t0);
     auto tile = [&](auto full_tag) {
@@ -334,57 +378,79 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kerne
           dd[i] = s_dt[buf][i][c];
         }
       }
+      if constexpr (AGG) {
 #pragma unroll
-      for (int i = 0; i < kTT; ++i) {
-        ys[i] = 0.0f;
-        if (kFull || i < tn) {
-          const float2 Bv = *reinterpret_cast<const float2*>(&s_B[buf][i][n0]);
-          const float2 Cv = *reinterpret_cast<const float2*>(&s_C[buf][i][n0]);
-          if (ck_b != nullptr && (i % kCK) == 0) {
-            const int blk = (t0 + i) / kCK;
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-              if (valid && n0 + j < N) st32(ck_b, (uint32_t)(blk * ND + (n0 + j) * D + d), h[j]);
+        for (int i = 0; i < kTT; ++i) {
+          if (kFull || i < tn) {
+            const float2 Bv = *reinterpret_cast<const float2*>(&s_B[buf][i][n0]);
+            const float w = dd[i] * uu[i];
+            h[0] = fmaf(fast_exp2(A2[0] * dd[i]), h[0], Bv.x * w);
+            h[1] = fmaf(fast_exp2(A2[1] * dd[i]), h[1], Bv.y * w);
+            dsum += dd[i];
           }
-          const float w = dd[i] * uu[i];
-          const float a0 = fast_exp2(A2[0] * dd[i]);
-          const float a1 = fast_exp2(A2[1] * dd[i]);
-          h[0] = fmaf(a0, h[0], Bv.x * w);
-          h[1] = fmaf(a1, h[1], Bv.y * w);
-          ys[i] = fmaf(Cv.y, h[1], Cv.x * h[0]);
         }
-      }
-      // add the two halves of each step's sum: even steps land in lanes < 32,
-      // odd steps in lanes >= 32
+      } else {
 #pragma unroll
-      for (int i = 0; i < kTT; i += 2)
-        if (kFull || i < tn) s_y[wave][i + hf][c] = half_pair(ys[i], ys[i + 1]);
+        for (int i = 0; i < kTT; ++i) {
+          ys[i] = 0.0f;
+          if (kFull || i < tn) {
+            const float2 Bv = *reinterpret_cast<const float2*>(&s_B[buf][i][n0]);
+            const float2 Cv = *reinterpret_cast<const float2*>(&s_C[buf][i][n0]);
+            if (ck_b != nullptr && (i % kCK) == 0) {
+              const int blk = (t0 + i) / kCK;
+#pragma unroll
+              for (int j = 0; j < 2; ++j)
+                if (valid && n0 + j < N) st32(ck_b, (uint32_t)(blk * ND + (n0 + j) * D + d), h[j]);
+            }
+            const float w = dd[i] * uu[i];
+            const float a0 = fast_exp2(A2[0] * dd[i]);
+            const float a1 = fast_exp2(A2[1] * dd[i]);
+            h[0] = fmaf(a0, h[0], Bv.x * w);
+            h[1] = fmaf(a1, h[1], Bv.y * w);
+            ys[i] = fmaf(Cv.y, h[1], Cv.x * h[0]);
+          }
+        }
+        // add the two halves of each step's sum: even steps land in lanes < 32,
+        // odd steps in lanes >= 32
+#pragma unroll
+        for (int i = 0; i < kTT; i += 2)
+          if (kFull || i < tn) s_y[wave][i + hf][c] = half_pair(ys[i], ys[i + 1]);
+      }
     };
     if (tn == kTT) tile(std::true_type{}); else tile(std::false_type{});
-    __syncthreads();
-    auto yreduce = [&](auto full_tag) {
-      constexpr bool kFull = decltype(full_tag)::value;
+    if constexpr (!AGG) {
+      __syncthreads();
+      auto yreduce = [&](auto full_tag) {
+        constexpr bool kFull = decltype(full_tag)::value;
 #pragma unroll
-      for (int k = 0; k < RPT; ++k) {
-        const int i = srow0 + k * RSTEP;
-        if (kFull || i < tn) {
-          float ys = 0.0f;
+        for (int k = 0; k < RPT; ++k) {
+          const int i = srow0 + k * RSTEP;
+          if (kFull || i < tn) {
+            float ys = 0.0f;
 #pragma unroll
-          for (int w = 0; w < NG; ++w) ys += s_y[w][i][scol];
-          const int t = t0 + i;
-          const int pt = rev ? L - 1 - t : t;
-          if (skip) ys = fmaf(stage_eu ? s_eu[buf][i][scol] : s_u[buf][i][scol], Dq, ys);
-          if (gate) {
-            const float zz = s_ez[buf][i][scol];
-            ys *= zz * sigmoid(zz);
+            for (int w = 0; w < NG; ++w) ys += s_y[w][i][scol];
+            const int t = t0 + i;
+            const int pt = rev ? L - 1 - t : t;
+            if (skip) ys = fmaf(stage_eu ? s_eu[buf][i][scol] : s_u[buf][i][scol], Dq, ys);
+            if (gate) {
+              const float zz = s_ez[buf][i][scol];
+              ys *= zz * sigmoid(zz);
+            }
+            on_valid_lanes(full_cb, svalid, [&] { st32(y_b, (uint32_t)(pt * D + sq), ys); });
           }
-          on_valid_lanes(full_cb, svalid, [&] { st32(y_b, (uint32_t)(pt * D + sq), ys); });
         }
-      }
-    };
-    if (tn == kTT) yreduce(std::true_type{}); else yreduce(std::false_type{});
+      };
+      if (tn == kTT) yreduce(std::true_type{}); else yreduce(std::false_type{});
+    }
     if (more) commit(buf ^ 1, t0 + kTT);
     __syncthreads();
+  }
+  if constexpr (AGG) {
+    const int64_t o = (int64_t)b * p.nseg + seg;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      if (valid && n0 + j < N) p.agg_H[(o * N + n0 + j) * D + d] = h[j];
+    if (wave == 0 && hf == 0 && valid) p.agg_S[o * D + d] = dsum;
   }
 }
 
@@ -406,10 +472,13 @@ struct BwdArgs {
   T* dz;
   float* ws_dB;   // [ncb][B][L][N]
   float* ws_dC;   // [ncb][B][L][N]
-  float* ws_dA;   // [B][D][N]
-  float* ws_dD;   // [B][D]
+  float* ws_dA;   // [B][nseg][D][N]
+  float* ws_dD;   // [B][nseg][D]
   float* ws_ddt;  // [ncb][B][L] (broadcast delta only)
+  float* agg_G;   // [B][nseg][N][D]: adjoint carry leaving each segment (leftwards) from a zero start
+  float* agg_S;   // [B][nseg][D]: sum of delta over each segment
   int Bt, L, D, N, nblk, ncb;
+  int seg_len, nseg;
   int dstride;
   uint32_t flags;
 };
@@ -432,7 +501,10 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
   const int hf = lane >> 5;
   const int b = blockIdx.y;
   const int cb = blockIdx.x;
+  const int seg = blockIdx.z;
   const int L = p.L, D = p.D, N = p.N;
+  const int blk_lo = seg * (p.seg_len / kCK);
+  const int blk_hi = min(p.nblk, blk_lo + p.seg_len / kCK);
   const int d = cb * kCh + c;
   const bool valid = d < D;
   const int dc = valid ? d : 0;
@@ -462,7 +534,31 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
     g[j] = 0.0f;
     dAacc[j] = 0.0f;
   }
+  if (seg < p.nseg - 1) {
+    // adjoint carry entering this segment from the right: fold the later
+    // segments' aggregates, last segment first (g = a_t f_t at each segment's
+    // first step is linear in the carry it receives)
+    const float* __restrict__ aS = p.agg_S + (int64_t)b * p.nseg * D + dc;
+    const float* __restrict__ aG = p.agg_G + (int64_t)b * p.nseg * N * D + dc;
+    const int nc0 = min(n0, N - 1), nc1 = min(n0 + 1, N - 1);
+#pragma unroll 4
+    for (int s = p.nseg - 1; s > seg; --s) {
+      const float sd = aS[(int64_t)s * D];
+      const float G0 = aG[((int64_t)s * N + nc0) * D];
+      const float G1 = aG[((int64_t)s * N + nc1) * D];
+      g[0] = fmaf(fast_exp2(A2[0] * sd), g[0], G0);
+      g[1] = fmaf(fast_exp2(A2[1] * sd), g[1], G1);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      if (!(valid && n0 + j < N)) g[j] = 0.0f;
+  }
+  // dA and dD are sums over every step of the row: per block (16 steps), per
+  // group of 16 blocks, then the total, so a 2^20-step row's total sees 4096
+  // fp32 adds instead of 2^20
+  float dAmid[2] = {0.0f, 0.0f};
   float dDacc = 0.0f;  // for column scol, over this thread's rows
+  float dDmid = 0.0f;
 
   __shared__ float s_u[2][kCK][kCh], s_dt[2][kCK][kCh], s_dy[2][kCK][kCh];
   __shared__ float s_go[EB][ER][kCh], s_gz[EB][ER][kCh];  // gate: raw dy and z at the output position
@@ -564,17 +660,17 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
     }
   };
 
-  fetch(p.nblk - 1);
-  commit(0, p.nblk - 1);
+  fetch(blk_hi - 1);
+  commit(0, blk_hi - 1);
   __syncthreads();
   int buf = 0;
   float h[2];
-  for (int blk = p.nblk - 1; blk >= 0; --blk, buf ^= 1) {
+  for (int blk = blk_hi - 1; blk >= blk_lo; --blk, buf ^= 1) {
     const int t0 = blk * kCK;
     const int tn = min(kCK, L - t0);
 #pragma unroll
     for (int j = 0; j < 2; ++j) h[j] = (valid && n0 + j < N) ? r_h[j] : 0.0f;
-    const bool more = blk > 0;
+    const bool more = blk > blk_lo;
     if (more) fetch(blk - 1);
 
     auto sweeps = [&](auto full_tag) {
@@ -630,6 +726,7 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
         if (i % kRB == kRB - 1 && (kFull || i - (kRB - 1) < tn)) flush(i - (kRB - 1), 1);
       }
       // adjoint, backwards through the block
+      float dAblk[2] = {0.0f, 0.0f};
 #pragma unroll
       for (int i = kCK - 1; i >= 0; --i) {
         if (i % kRB == kRB - 1) {
@@ -649,7 +746,7 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
             const float gg = a_s[i][j] * f;
             const float qv = gg * hp_s[i][j];
             s2 = fmaf(Av[j], qv, s2);
-            dAacc[j] = fmaf(dd[i], qv, dAacc[j]);
+            dAblk[j] = fmaf(dd[i], qv, dAblk[j]);
             s1 = fmaf(Bn[j], f, s1);
             xb[i % kRB][j] = f * w;
             g[j] = gg;
@@ -659,6 +756,8 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
         }
         if (i % kRB == 0 && (kFull || i < tn)) flush(i, 0);
       }
+      dAmid[0] += dAblk[0];
+      dAmid[1] += dAblk[1];
     };
     if (tn == kCK) sweeps(std::true_type{}); else sweeps(std::false_type{});
     __syncthreads();
@@ -666,6 +765,7 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
     // combine the per-wave partials; write du, ddelta (and dz)
     auto combine = [&](auto full_tag) {
       constexpr bool kFull = decltype(full_tag)::value;
+      float dDblk = 0.0f;  // per block, like dA
 #pragma unroll
       for (int k = 0; k < RPT; ++k) {
         const int i = srow0 + k * RSTEP;
@@ -682,7 +782,7 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
             // y_out[t,d] holds u[t,d]*D[d] (selectssm.py:238): its gradient lands on u[t,d]
             const float dyo = stage_dyo ? s_dyo[buf][i][scol] : s_dy[buf][i][scol];
             du = fmaf(Dd, dyo, du);
-            dDacc = fmaf(dyo, uu, dDacc);
+            dDblk = fmaf(dyo, uu, dDblk);
           }
           on_valid_lanes(full_cb, svalid, [&] {
             st32(du_b, (uint32_t)(t * D + sdc), du);
@@ -705,8 +805,15 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
           }
         }
       }
+      dDmid += dDblk;
     };
     if (tn == kCK) combine(std::true_type{}); else combine(std::false_type{});
+    if (((blk - blk_lo) & 15) == 0) {  // close a group of 16 blocks (and the row's last group)
+      dAacc[0] += dAmid[0];
+      dAacc[1] += dAmid[1];
+      dDacc += dDmid;
+      dAmid[0] = dAmid[1] = dDmid = 0.0f;
+    }
     // dB, dC totals of this channel block, coalesced
     {
       float* __restrict__ wB = p.ws_dB + (((int64_t)cb * p.Bt + b) * L + t0) * N;
@@ -731,7 +838,7 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int n = n0 + j;
-    if (valid && n < N) p.ws_dA[((int64_t)b * D + d) * N + n] = dAacc[j];
+    if (valid && n < N) p.ws_dA[(((int64_t)b * p.nseg + seg) * D + d) * N + n] = dAacc[j];
   }
   if (skip) {
     // dD partial: the threads of one column accumulated disjoint rows
@@ -742,9 +849,155 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
       float sacc = 0.0f;
 #pragma unroll
       for (int r = 0; r < RSTEP; ++r) sacc += dred[r][tid];
-      p.ws_dD[(int64_t)b * D + sd] = sacc;
+      p.ws_dD[((int64_t)b * p.nseg + seg) * D + sd] = sacc;
     }
   }
+}
+
+// Aggregate pass of a time-split backward.  Workgroup (cb, b, seg - 1), for
+// segments seg >= 1, walks its segment backwards with no carry from the right
+// and writes the carry it hands to the segment on its left, a_t f_t at the
+// segment's first step t (f_t = C_t dy_t + a_{t+1} f_{t+1}, ssmrecscan.py:96-100,
+// 150-153), and the segment's sum of delta.  The carry a segment receives
+// from the right enters that value as exp(A * sum delta) * carry.
+template <int NG, bool EPI, typename T>
+__global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_agg_kernel(BwdArgs<T> p) {
+  constexpr int NS = NG * kSPW;
+  constexpr int NT = kWave * NG;
+  constexpr int RPT = kTT * kCh / NT;
+  constexpr int RSTEP = NT / kCh;
+  constexpr int BCE = kTT * NS / NT;
+  static_assert(BCE * NT == kTT * NS && RPT * NT == kTT * kCh, "staging must tile exactly");
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & (kCh - 1);
+  const int hf = lane >> 5;
+  const int b = blockIdx.y;
+  const int cb = blockIdx.x;
+  const int seg = blockIdx.z + 1;
+  const int L = p.L, D = p.D, N = p.N;
+  const int t_lo = seg * p.seg_len;
+  const int t_hi = min(L, t_lo + p.seg_len);
+  const int d = cb * kCh + c;
+  const bool valid = d < D;
+  const int dc = valid ? d : 0;
+  const int n0 = wave * kSPW + 2 * hf;
+  const bool rev = p.flags & SSM_REVERSE;
+  const bool comp = rev && (p.flags & SSM_COMPLEMENT);
+  const bool gate = EPI && (p.flags & SSM_GATE);
+  const int scol = tid & (kCh - 1);
+  const int srow0 = tid / kCh;
+  const int sd = cb * kCh + scol;
+  const bool svalid = sd < D;
+  const int sdc = svalid ? sd : 0;
+  const int sq = comp ? D - 1 - sdc : sdc;
+
+  float A2[2], g[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int n = n0 + j;
+    A2[j] = (valid && n < N) ? p.A[(int64_t)dc * N + n] * kLog2e : 0.0f;
+    g[j] = 0.0f;
+  }
+  float dsum = 0.0f;
+
+  __shared__ float s_dt[2][kTT][kCh], s_dy[2][kTT][kCh];
+  __shared__ __attribute__((aligned(16))) float s_C[2][kTT][NS];
+
+  const int64_t bLD = (int64_t)b * L * D;
+  const int64_t bLN = (int64_t)b * L * N;
+  const int dtD = p.dstride ? D : 1;
+  const int scol_dt = p.dstride ? sdc : 0;
+  const T* __restrict__ dt_b = p.delta + (int64_t)b * L * dtD;
+  const T* __restrict__ dy_b = p.dy + bLD;
+  const T* __restrict__ z_b = EPI ? p.z + bLD : nullptr;
+  const T* __restrict__ C_b = p.Cc + bLN;
+  const int LN = L * N;
+
+  float r_dt[RPT], r_dy[RPT], r_gz[RPT], r_C[BCE];
+  auto fetch = [&](int t0) {
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      const int tc = min(t0 + srow0 + k * RSTEP, L - 1);
+      const int pr = rev ? L - 1 - tc : tc;
+      r_dt[k] = ld32(dt_b, (uint32_t)(tc * dtD + scol_dt));
+      r_dy[k] = ld32(dy_b, (uint32_t)(pr * D + sq));
+      if (gate) r_gz[k] = ld32(z_b, (uint32_t)(pr * D + sq));
+    }
+#pragma unroll
+    for (int k = 0; k < BCE; ++k) {
+      const int e = tid + k * NT;
+      int gi;
+      if (NS == N) {
+        gi = t0 * N + e;
+      } else {
+        const int i = e / NS, n = e - i * NS;
+        gi = (t0 + i) * N + min(n, N - 1);
+      }
+      r_C[k] = ld32(C_b, (uint32_t)min(gi, LN - 1));
+    }
+  };
+  auto commit = [&](int buf, int t0) {
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      const int i = srow0 + k * RSTEP;
+      const bool in = svalid && t0 + i < L;
+      s_dt[buf][i][scol] = in ? r_dt[k] : 0.0f;
+      const float go = in ? r_dy[k] : 0.0f;
+      if (gate) {
+        const float gz = in ? r_gz[k] : 0.0f;
+        s_dy[buf][i][scol] = go * gz * sigmoid(gz);  // as the main backward pass stages it
+      } else {
+        s_dy[buf][i][scol] = go;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < BCE; ++k) {
+      const int e = tid + k * NT;
+      const int i = e / NS, n = e - (e / NS) * NS;
+      (&s_C[buf][0][0])[e] = (t0 + i < L && n < N) ? r_C[k] : 0.0f;
+    }
+  };
+
+  const int t_last = t_lo + (t_hi - 1 - t_lo) / kTT * kTT;
+  fetch(t_last);
+  commit(0, t_last);
+  __syncthreads();
+  int buf = 0;
+  for (int t0 = t_last; t0 >= t_lo; t0 -= kTT, buf ^= 1) {
+    const bool more = t0 > t_lo;
+    if (more) fetch(t0 - kTT);
+    const int tn = min(kTT, L - t0);
+    auto tile = [&](auto full_tag) {
+      constexpr bool kFull = decltype(full_tag)::value;
+      float dd[kTT], dyv[kTT];
+#pragma unroll
+      for (int i = 0; i < kTT; ++i) {
+        if (kFull || i < tn) {
+          dd[i] = s_dt[buf][i][c];
+          dyv[i] = s_dy[buf][i][c];
+        }
+      }
+#pragma unroll
+      for (int i = kTT - 1; i >= 0; --i) {
+        if (kFull || i < tn) {
+          const float2 Cv = *reinterpret_cast<const float2*>(&s_C[buf][i][n0]);
+          g[0] = fast_exp2(A2[0] * dd[i]) * fmaf(Cv.x, dyv[i], g[0]);
+          g[1] = fast_exp2(A2[1] * dd[i]) * fmaf(Cv.y, dyv[i], g[1]);
+          dsum += dd[i];
+        }
+      }
+    };
+    if (tn == kTT) tile(std::true_type{}); else tile(std::false_type{});
+    if (more) commit(buf ^ 1, t0 - kTT);
+    __syncthreads();
+  }
+  const int64_t o = (int64_t)b * p.nseg + seg;
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    if (valid && n0 + j < N) p.agg_G[(o * N + n0 + j) * D + d] = g[j];
+  if (wave == 0 && hf == 0 && valid) p.agg_S[o * D + d] = dsum;
 }
 
 // out[i] = sum_k ws[k*count + i], k = 0..nparts-1 in order
@@ -776,7 +1029,30 @@ struct Shape {
   int B, L, D, N, nblk, ncb;
   int NG;    // waves per workgroup (4 states each)
   bool epi;  // skip / gate epilogue fused
+  int seg_len, nseg;  // time segments per row
 };
+
+// Automatic time split: a row is split only when the unsplit grid would leave
+// more than half of the resident-wave slots empty (256 CUs x 4 SIMDs x 2 waves
+// of these kernels on MI355X), into enough segments to fill them, each at
+// least kMinAutoSeg steps long.  The choice depends on the desc alone, so a
+// given desc always computes in the same order.
+constexpr int kFillWaves = 2048;
+constexpr int kMinAutoSeg = 512;
+constexpr int kMaxSeg = 1024;
+
+void choose_segments(const ssm_desc_t* desc, Shape* s) {
+  int64_t want = desc->segments;
+  if (want == 0) {
+    const int64_t waves = (int64_t)s->B * s->ncb * s->NG;
+    want = 2 * waves >= kFillWaves ? 1 : (kFillWaves + waves - 1) / waves;
+    want = std::min<int64_t>(want, std::max(1, s->L / kMinAutoSeg));
+  }
+  int64_t len = (s->L + want - 1) / want;
+  len = (len + kTT - 1) / kTT * kTT;  // segments start on forward tiles
+  s->seg_len = (int)len;
+  s->nseg = (int)((s->L + len - 1) / len);
+}
 
 int validate(const ssm_desc_t* desc, Shape* s) {
   if (desc == nullptr) return fail(SSM_ERR_INVALID, "desc is NULL");
@@ -796,7 +1072,7 @@ int validate(const ssm_desc_t* desc, Shape* s) {
     return fail(SSM_ERR_INVALID, "SSM_COMPLEMENT requires SSM_REVERSE (selectssm.py:116)");
   if (desc->delta_broadcast != 0 && desc->delta_broadcast != 1)
     return fail(SSM_ERR_INVALID, "delta_broadcast must be 0 or 1");
-  if (desc->reserved != 0) return fail(SSM_ERR_INVALID, "reserved must be 0");
+  if (desc->segments < 0 || desc->segments > kMaxSeg) return fail(SSM_ERR_INVALID, "segments must be in 0..1024");
   s->B = (int)desc->batch;
   s->L = (int)desc->seqlen;
   s->D = (int)desc->dim;
@@ -807,6 +1083,7 @@ int validate(const ssm_desc_t* desc, Shape* s) {
   const int ng = (s->N + kSPW - 1) / kSPW;
   s->NG = 1;
   while (s->NG < ng) s->NG *= 2;  // instantiated wave counts: 1, 2, 4, 8
+  choose_segments(desc, s);
   return SSM_OK;
 }
 
@@ -827,26 +1104,33 @@ bool dispatch_variant(const Shape& s, F&& f) {
 
 size_t ckpt_floats(const Shape& s) { return (size_t)s.B * s.nblk * s.N * s.D; }
 
+// Per-segment aggregates of a time-split scan: [B][nseg][N][D] states (or
+// adjoint carries) then [B][nseg][D] delta sums.  None for one segment.
+size_t agg_floats(const Shape& s) { return s.nseg > 1 ? (size_t)s.B * s.nseg * (s.N + 1) * s.D : 0; }
+
 struct WsLayout {
-  size_t dB, dC, dA, dD, ddt, total;  // float offsets
+  size_t dB, dC, dA, dD, ddt, aggG, aggS, total;  // float offsets
 };
 
 WsLayout ws_layout(const Shape& s, bool bcast) {
   WsLayout w{};
   const size_t bc = (size_t)s.ncb * s.B * s.L * s.N;
+  const size_t parts = (size_t)s.B * s.nseg;  // dA, dD partials: one per (batch row, segment)
   w.dB = 0;
   w.dC = w.dB + bc;
   w.dA = w.dC + bc;
-  w.dD = w.dA + (size_t)s.B * s.D * s.N;
-  w.ddt = w.dD + (size_t)s.B * s.D;
-  w.total = w.ddt + (bcast ? (size_t)s.ncb * s.B * s.L : 0);
+  w.dD = w.dA + parts * s.D * s.N;
+  w.ddt = w.dD + parts * s.D;
+  w.aggG = w.ddt + (bcast ? (size_t)s.ncb * s.B * s.L : 0);
+  w.aggS = w.aggG + (s.nseg > 1 ? parts * s.N * s.D : 0);
+  w.total = w.aggG + agg_floats(s);
   return w;
 }
 
 template <typename T>
 int launch_fwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const void* u, const void* delta,
                const float* A, const void* Bc, const void* Cc, const float* Dskip, const void* z, void* y,
-               float* ckpt) {
+               float* ckpt, void* workspace) {
   FwdArgs<T> a;
   a.u = static_cast<const T*>(u);
   a.delta = static_cast<const T*>(delta);
@@ -857,17 +1141,23 @@ int launch_fwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const voi
   a.z = static_cast<const T*>(z);
   a.y = static_cast<T*>(y);
   a.ckpt = ckpt;
+  a.agg_H = static_cast<float*>(workspace);
+  a.agg_S = a.agg_H + (s.nseg > 1 ? (size_t)s.B * s.nseg * s.N * s.D : 0);
   a.L = s.L;
   a.D = s.D;
   a.N = s.N;
   a.nblk = s.nblk;
+  a.seg_len = s.seg_len;
+  a.nseg = s.nseg;
   a.dstride = desc->delta_broadcast ? 0 : 1;
   a.flags = desc->flags;
-  dim3 grid(s.ncb, s.B);
   if (!dispatch_variant(s, [&](auto ng, auto epi) {
         constexpr int G = decltype(ng)::value;
         constexpr bool E = decltype(epi)::value;
-        hipLaunchKernelGGL((ssm_fwd_kernel<G, E, T>), grid, dim3(kWave * G), 0, st, a);
+        if (s.nseg > 1)  // aggregates of every segment but the last
+          hipLaunchKernelGGL((ssm_fwd_kernel<G, false, true, T>), dim3(s.ncb, s.B, s.nseg - 1), dim3(kWave * G), 0,
+                             st, a);
+        hipLaunchKernelGGL((ssm_fwd_kernel<G, E, false, T>), dim3(s.ncb, s.B, s.nseg), dim3(kWave * G), 0, st, a);
       }))
     return fail(SSM_ERR_UNSUPPORTED, "no kernel variant for this shape");
   return hip_check(hipGetLastError(), "ssm_fwd launch");
@@ -899,19 +1189,24 @@ int launch_bwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const voi
   a.ws_dA = ws + wl.dA;
   a.ws_dD = ws + wl.dD;
   a.ws_ddt = ws + wl.ddt;
+  a.agg_G = ws + wl.aggG;
+  a.agg_S = ws + wl.aggS;
   a.Bt = s.B;
   a.L = s.L;
   a.D = s.D;
   a.N = s.N;
   a.nblk = s.nblk;
   a.ncb = s.ncb;
+  a.seg_len = s.seg_len;
+  a.nseg = s.nseg;
   a.dstride = bcast ? 0 : 1;
   a.flags = desc->flags;
-  dim3 grid(s.ncb, s.B);
   if (!dispatch_variant(s, [&](auto ng, auto epi) {
         constexpr int G = decltype(ng)::value;
         constexpr bool E = decltype(epi)::value;
-        hipLaunchKernelGGL((ssm_bwd_kernel<G, E, T>), grid, dim3(kWave * G), 0, st, a);
+        if (s.nseg > 1)  // adjoint aggregates of every segment but the first
+          hipLaunchKernelGGL((ssm_bwd_agg_kernel<G, E, T>), dim3(s.ncb, s.B, s.nseg - 1), dim3(kWave * G), 0, st, a);
+        hipLaunchKernelGGL((ssm_bwd_kernel<G, E, T>), dim3(s.ncb, s.B, s.nseg), dim3(kWave * G), 0, st, a);
       }))
     return fail(SSM_ERR_UNSUPPORTED, "no kernel variant for this shape");
   int rc = hip_check(hipGetLastError(), "ssm_bwd launch");
@@ -926,8 +1221,8 @@ int launch_bwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const voi
   const int64_t bln = (int64_t)s.B * s.L * s.N;
   reduce(ws + wl.dB, static_cast<T*>(dB), s.ncb, bln);
   reduce(ws + wl.dC, static_cast<T*>(dC), s.ncb, bln);
-  reduce(ws + wl.dA, dA, s.B, (int64_t)s.D * s.N);
-  if (desc->flags & SSM_SKIP) reduce(ws + wl.dD, dD, s.B, (int64_t)s.D);
+  reduce(ws + wl.dA, dA, s.B * s.nseg, (int64_t)s.D * s.N);
+  if (desc->flags & SSM_SKIP) reduce(ws + wl.dD, dD, s.B * s.nseg, (int64_t)s.D);
   if (bcast) reduce(ws + wl.ddt, static_cast<T*>(ddelta), s.ncb, (int64_t)s.B * s.L);
   return hip_check(hipGetLastError(), "ssm_bwd reduce launch");
 }
@@ -943,29 +1238,40 @@ int ssm_abi_version(void) { return SSM_ABI_VERSION; }
 const char* ssm_last_error(void) { return g_last_error.c_str(); }
 
 size_t ssm_ckpt_bytes(const ssm_desc_t* desc) {
+  g_last_error.clear();
   Shape s;
   if (validate(desc, &s)) return 0;
   return ckpt_floats(s) * sizeof(float);
 }
 
+size_t ssm_fwd_workspace_bytes(const ssm_desc_t* desc) {
+  g_last_error.clear();
+  Shape s;
+  if (validate(desc, &s)) return 0;
+  return agg_floats(s) * sizeof(float);
+}
+
 size_t ssm_bwd_workspace_bytes(const ssm_desc_t* desc) {
+  g_last_error.clear();
   Shape s;
   if (validate(desc, &s)) return 0;
   return ws_layout(s, desc->delta_broadcast != 0).total * sizeof(float);
 }
 
 int ssm_fwd(void* stream, const ssm_desc_t* desc, const void* u, const void* delta, const float* A,
-            const void* Bc, const void* Cc, const float* Dskip, const void* z, void* y, float* ckpt) {
+            const void* Bc, const void* Cc, const float* Dskip, const void* z, void* y, float* ckpt,
+            void* workspace) {
   g_last_error.clear();
   Shape s;
   if (int rc = validate(desc, &s)) return rc;
   if (!u || !delta || !A || !Bc || !Cc || !y) return fail(SSM_ERR_INVALID, "ssm_fwd: required pointer is NULL");
+  if (s.nseg > 1 && !workspace) return fail(SSM_ERR_INVALID, "ssm_fwd: workspace is NULL but ssm_fwd_workspace_bytes > 0");
   if ((desc->flags & SSM_SKIP) && !Dskip) return fail(SSM_ERR_INVALID, "SSM_SKIP needs Dskip");
   if ((desc->flags & SSM_GATE) && !z) return fail(SSM_ERR_INVALID, "SSM_GATE needs z");
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (desc->dtype == SSM_F32)
-    return launch_fwd<float>(st, desc, s, u, delta, A, Bc, Cc, Dskip, z, y, ckpt);
-  return launch_fwd<bf16>(st, desc, s, u, delta, A, Bc, Cc, Dskip, z, y, ckpt);
+    return launch_fwd<float>(st, desc, s, u, delta, A, Bc, Cc, Dskip, z, y, ckpt, workspace);
+  return launch_fwd<bf16>(st, desc, s, u, delta, A, Bc, Cc, Dskip, z, y, ckpt, workspace);
 }
 
 int ssm_bwd(void* stream, const ssm_desc_t* desc, const void* u, const void* delta, const float* A,

@@ -109,38 +109,40 @@ def _flags(skip, gate, reverse, complement):
     return f
 
 
-def _desc(u, delta, A, flags):
+def _desc(u, delta, A, flags, segments=0):
     Bt, Ln, D = u.shape
     return L.make_desc(Bt, Ln, D, A.shape[1], _IO_DTYPES[u.dtype], flags,
-                       delta_broadcast=(delta.shape[-1] == 1 and D != 1))
+                       delta_broadcast=(delta.shape[-1] == 1 and D != 1), segments=segments)
+
+
+def _scratch(nbytes, device):
+    return torch.empty(nbytes // 4, dtype=torch.float32, device=device) if nbytes else None
 
 
 # ------------------------------------------------------------- raw launchers
 
-def scan_fwd(u, delta, A, B, C, Dskip=None, z=None, reverse=False, complement=False, want_ckpt=True):
+def scan_fwd(u, delta, A, B, C, Dskip=None, z=None, reverse=False, complement=False, want_ckpt=True,
+             segments=0):
     """Run ``ssm_fwd``.  All tensors contiguous, on one GPU, I/O dtype shared.
 
+    ``segments`` splits each row's time axis (0: chosen from the shape).
     Returns ``(y, ckpt)``; ``ckpt`` is None when ``want_ckpt`` is False.
     """
     flags = _flags(Dskip is not None, z is not None, reverse, complement)
-    desc = _desc(u, delta, A, flags)
+    desc = _desc(u, delta, A, flags, segments)
     lib = L.lib()
     y = torch.empty_like(u)
-    ckpt = None
-    if want_ckpt:
-        nbytes = lib.ssm_ckpt_bytes(ctypes.byref(desc))
-        if nbytes == 0:
-            L.check(L.SSM_ERR_INVALID)
-        ckpt = torch.empty(nbytes // 4, dtype=torch.float32, device=u.device)
+    ckpt = _scratch(L.size_query(lib.ssm_ckpt_bytes, desc), u.device) if want_ckpt else None
+    ws = _scratch(L.size_query(lib.ssm_fwd_workspace_bytes, desc, allow_zero=True), u.device)
     L.check(lib.ssm_fwd(_stream(), ctypes.byref(desc), _ptr(u), _ptr(delta), _ptr(A), _ptr(B), _ptr(C),
-                        _ptr(Dskip), _ptr(z), _ptr(y), _ptr(ckpt)))
+                        _ptr(Dskip), _ptr(z), _ptr(y), _ptr(ckpt), _ptr(ws)))
     return y, ckpt
 
 
-def scan_bwd(u, delta, A, B, C, Dskip, z, ckpt, dy, reverse=False, complement=False):
+def scan_bwd(u, delta, A, B, C, Dskip, z, ckpt, dy, reverse=False, complement=False, segments=0):
     """Run ``ssm_bwd``.  Returns ``(du, ddelta, dA, dB, dC, dD, dz)`` (dD / dz None when unused)."""
     flags = _flags(Dskip is not None, z is not None, reverse, complement)
-    desc = _desc(u, delta, A, flags)
+    desc = _desc(u, delta, A, flags, segments)
     lib = L.lib()
     du = torch.empty_like(u)
     ddelta = torch.empty_like(delta)
@@ -149,10 +151,7 @@ def scan_bwd(u, delta, A, B, C, Dskip, z, ckpt, dy, reverse=False, complement=Fa
     dC = torch.empty_like(C)
     dD = torch.empty_like(Dskip) if Dskip is not None else None
     dz = torch.empty_like(z) if z is not None else None
-    nbytes = lib.ssm_bwd_workspace_bytes(ctypes.byref(desc))
-    if nbytes == 0:
-        L.check(L.SSM_ERR_INVALID)
-    ws = torch.empty(nbytes // 4, dtype=torch.float32, device=u.device)
+    ws = _scratch(L.size_query(lib.ssm_bwd_workspace_bytes, desc), u.device)
     L.check(lib.ssm_bwd(_stream(), ctypes.byref(desc), _ptr(u), _ptr(delta), _ptr(A), _ptr(B), _ptr(C),
                         _ptr(Dskip), _ptr(z), _ptr(ckpt), _ptr(dy), _ptr(du), _ptr(ddelta), _ptr(dA),
                         _ptr(dB), _ptr(dC), _ptr(dD), _ptr(dz), _ptr(ws)))
@@ -170,22 +169,24 @@ class SelectiveScanFn(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, u, delta, A, B, C, Dskip, z, reverse, complement):
+    def forward(ctx, u, delta, A, B, C, Dskip, z, reverse, complement, segments=0):
         y, ckpt = scan_fwd(u, delta, A, B, C, Dskip, z, reverse, complement,
-                           want_ckpt=torch.is_grad_enabled() or any(ctx.needs_input_grad))
+                           want_ckpt=torch.is_grad_enabled() or any(ctx.needs_input_grad), segments=segments)
         ctx.save_for_backward(u, delta, A, B, C, Dskip, z, ckpt)
         ctx.flags = (reverse, complement)
+        ctx.segments = segments
         return y
 
     @staticmethod
     def backward(ctx, dy):
         u, delta, A, B, C, Dskip, z, ckpt = ctx.saved_tensors
         dy = dy.to(u.dtype).contiguous()
-        du, ddelta, dA, dB, dC, dD, dz = scan_bwd(u, delta, A, B, C, Dskip, z, ckpt, dy, *ctx.flags)
-        return du, ddelta, dA, dB, dC, dD, dz, None, None
+        du, ddelta, dA, dB, dC, dD, dz = scan_bwd(u, delta, A, B, C, Dskip, z, ckpt, dy, *ctx.flags,
+                                                  segments=ctx.segments)
+        return du, ddelta, dA, dB, dC, dD, dz, None, None, None
 
 
-def selective_scan(u, delta, A, B, C, D=None, z=None, reverse=False, complement=False):
+def selective_scan(u, delta, A, B, C, D=None, z=None, reverse=False, complement=False, segments=0):
     """Fused selective scan with the SelectiveSSM / BidirectionalMamba epilogue.
 
     u, delta, B, C are in the scan domain (flipped already when ``reverse``,
@@ -196,6 +197,9 @@ def selective_scan(u, delta, A, B, C, D=None, z=None, reverse=False, complement=
         y = y + u * D          if D is given     (selectssm.py:238; u stays flipped)
         y = y * silu(z)        if z is given     (selectssm.py:335-336)
     ``complement`` (with ``reverse``) also mirrors the channel axis.
+    ``segments`` > 0 forces that many time segments per row (0: the library
+    splits rows only when there are too few to fill the GPU); the result
+    agrees with one segment up to fp32 rounding.
     """
     Bt, Ln, Dm, N = _check_shapes(u, delta, A, B, C, D, z)
     if complement and not reverse:
@@ -203,8 +207,10 @@ def selective_scan(u, delta, A, B, C, D=None, z=None, reverse=False, complement=
     io = _io_dtype(u, delta, B, C, z)
     cast = lambda t: None if t is None else t.to(io).contiguous()
     fcast = lambda t: None if t is None else t.to(torch.float32).contiguous()
+    if not 0 <= int(segments) <= 1024:
+        raise ValueError(f"segments must be in 0..1024, got {segments}")
     return SelectiveScanFn.apply(cast(u), cast(delta), fcast(A), cast(B), cast(C), fcast(D), cast(z),
-                                 bool(reverse), bool(complement))
+                                 bool(reverse), bool(complement), int(segments))
 
 
 # ------------------------------------------------------- reference-named API

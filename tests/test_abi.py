@@ -49,17 +49,52 @@ def test_size_queries():
     assert b"dstate" in lib.ssm_last_error()
 
 
+def fwd_ws(**kw):
+    lib = L.lib()
+    return L.size_query(lib.ssm_fwd_workspace_bytes, L.make_desc(**kw), allow_zero=True)
+
+
+def test_time_split_workspace_follows_the_segment_rule():
+    # enough rows to fill the chip: one segment, no forward workspace
+    assert fwd_ws(batch=8, seqlen=8192, dim=2048, dstate=16) == 0
+    assert fwd_ws(batch=16, seqlen=4096, dim=5120, dstate=16, dtype=L.SSM_BF16) == 0
+    # long-sequence shapes split in time: B*ceil(D/32)*ceil(N/4) waves, 2048 slots
+    # config 3 (1 x 1M x 1024): 128 waves -> 16 segments; config 2 per direction: 256 -> 8
+    per_seg = lambda B, N, D: B * (N + 1) * D * 4
+    assert fwd_ws(batch=1, seqlen=1 << 20, dim=1024, dstate=16) == 16 * per_seg(1, 16, 1024)
+    assert fwd_ws(batch=4, seqlen=131072, dim=512, dstate=16) == 8 * per_seg(4, 16, 512)
+    # segments never shorter than 512 steps when chosen automatically
+    assert fwd_ws(batch=1, seqlen=1024, dim=32, dstate=4) == 2 * per_seg(1, 4, 32)
+    assert fwd_ws(batch=1, seqlen=511, dim=32, dstate=4) == 0
+    # forced: 3 segments of L=100 round to 64-step segments (whole 32-step tiles) -> 2
+    assert fwd_ws(batch=2, seqlen=100, dim=8, dstate=4, segments=3) == 2 * per_seg(2, 4, 8)
+    assert fwd_ws(batch=2, seqlen=100, dim=8, dstate=4, segments=1) == 0
+    lib = L.lib()
+    d1 = L.make_desc(2, 100, 8, 4, segments=1)
+    d3 = L.make_desc(2, 100, 8, 4, segments=3)
+    # the backward also holds per-segment dA / dD partials and adjoint carries
+    assert lib.ssm_bwd_workspace_bytes(ctypes.byref(d3)) > lib.ssm_bwd_workspace_bytes(ctypes.byref(d1))
+
+
+def test_split_forward_needs_its_workspace():
+    lib = L.lib()
+    d = L.make_desc(2, 100, 8, 4, segments=3)
+    p = ctypes.c_void_p(16)
+    assert lib.ssm_fwd(None, ctypes.byref(d), p, p, p, p, p, None, None, p, None, None) == L.SSM_ERR_INVALID
+    assert b"workspace" in lib.ssm_last_error()
+
+
 @pytest.mark.parametrize("field,value,msg", [
     ("batch", 0, b"batch, seqlen and dim"), ("dstate", 0, b"dstate"), ("dtype", 7, b"dtype"),
     ("flags", 64, b"unknown flag"), ("flags", 2, b"COMPLEMENT requires"), ("delta_broadcast", 3, b"delta_broadcast"),
-    ("reserved", 1, b"reserved"),
+    ("segments", -1, b"segments"), ("segments", 1025, b"segments"),
 ])
 def test_invalid_desc_is_rejected_before_any_launch(field, value, msg):
     lib = L.lib()
     d = L.make_desc(2, 64, 64, 16)
     setattr(d, field, value)
     p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
-    rc = lib.ssm_fwd(None, ctypes.byref(d), p, p, p, p, p, None, None, p, None)
+    rc = lib.ssm_fwd(None, ctypes.byref(d), p, p, p, p, p, None, None, p, None, None)
     assert rc == L.SSM_ERR_INVALID
     assert msg in lib.ssm_last_error()
 
@@ -68,11 +103,11 @@ def test_null_pointers_and_missing_epilogue_operands_are_rejected():
     lib = L.lib()
     d = L.make_desc(2, 64, 64, 16)
     p = ctypes.c_void_p(16)
-    assert lib.ssm_fwd(None, ctypes.byref(d), None, p, p, p, p, None, None, p, None) == L.SSM_ERR_INVALID
+    assert lib.ssm_fwd(None, ctypes.byref(d), None, p, p, p, p, None, None, p, None, None) == L.SSM_ERR_INVALID
     d.flags = L.SSM_SKIP
-    assert lib.ssm_fwd(None, ctypes.byref(d), p, p, p, p, p, None, None, p, None) == L.SSM_ERR_INVALID
+    assert lib.ssm_fwd(None, ctypes.byref(d), p, p, p, p, p, None, None, p, None, None) == L.SSM_ERR_INVALID
     assert b"Dskip" in lib.ssm_last_error()
     d.flags = L.SSM_GATE
     rc = lib.ssm_bwd(None, ctypes.byref(d), p, p, p, p, p, None, p, p, p, p, p, p, p, p, None, None, p)
     assert rc == L.SSM_ERR_INVALID and b"dz" in lib.ssm_last_error()
-    assert lib.ssm_fwd(None, None, p, p, p, p, p, None, None, p, None) == L.SSM_ERR_INVALID
+    assert lib.ssm_fwd(None, None, p, p, p, p, p, None, None, p, None, None) == L.SSM_ERR_INVALID

@@ -1,0 +1,191 @@
+"""Time-split scans (a row's time axis in segments joined by carries) on the GPU.
+
+* forced segment counts against the fp64 oracle, every epilogue flag, fp32 and
+  bf16, delta broadcast, ragged last segments (rtol 1e-4 / atol 1e-5);
+* the automatic split of a long row against the fp64 oracle;
+* split and unsplit runs of the same inputs agree (rtol 1e-4 / atol 1e-5);
+* the config-3 shape (B=1, L=2^20, D=1024, N=16), split automatically into 16
+  segments: exact linearity, agreement with the unsplit run, and channels 0-15
+  and 1008-1023 against the float64 build of the C port of the reference's
+  algorithm, run as one sequential pass (min_recursion_length = L).  dA there
+  is a sum over 2^20 steps; float64 keeps the oracle's own rounding out of
+  the comparison.
+"""
+import numpy as np
+import pytest
+
+from oracle import ssm_oracle as O
+from selectssm_amd.synthetic import make_inputs
+
+from test_gpu_scan import RTOL, ATOL, _close, _cuda, _oracle
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(inp, flags=(), dtype=torch.float32, segments=0):
+    from selectssm_amd import selective_scan
+
+    t = {k: _cuda(v) for k, v in inp.items()}
+    for k in ("u", "dt", "B", "C", "z"):
+        t[k] = t[k].to(dtype).requires_grad_(True)
+    t["A"].requires_grad_(True)
+    t["D"].requires_grad_(True)
+    y = selective_scan(t["u"], t["dt"], t["A"], t["B"], t["C"], D=t["D"] if "skip" in flags else None,
+                       z=t["z"] if "gate" in flags else None, reverse="reverse" in flags,
+                       complement="complement" in flags, segments=segments)
+    y.backward(t["g"].to(dtype))
+    torch.cuda.synchronize()
+    return y, {k: t[k].grad for k in ("u", "dt", "A", "B", "C", "D", "z")}
+
+
+FLAGS = [(), ("skip",), ("gate",), ("reverse",), ("reverse", "complement", "skip", "gate"), ("reverse", "skip")]
+
+
+@pytest.mark.parametrize("shape,segments", [
+    ((2, 300, 40, 5), 4),      # 96-step segments, last one 12 steps
+    ((1, 1000, 70, 16), 7),    # ragged channel block, 160-step segments
+    ((2, 96, 8, 4), 3),        # 32-step segments (one tile each)
+    ((3, 257, 33, 2), 9),      # N=2, last segment a single step
+])
+@pytest.mark.parametrize("flags", FLAGS, ids=lambda f: "+".join(f) or "plain")
+def test_forced_segments_match_oracle(shape, segments, flags):
+    print(f"segments={segments} shape={shape} flags={flags}", flush=True)
+    inp = make_inputs(*shape, seed=11)
+    y, g = _run(inp, flags, segments=segments)
+    yr, gr = _oracle(inp, flags)
+    _close("y", y, yr)
+    for k in ("u", "dt", "A", "B", "C"):
+        _close(f"d{k}", g[k], gr[k])
+    if "skip" in flags:
+        _close("dD", g["D"], gr["D"])
+    if "gate" in flags:
+        _close("dz", g["z"], gr["z"])
+
+
+def test_forced_segments_delta_broadcast():
+    inp = make_inputs(2, 200, 24, 4, seed=5, delta_broadcast=True)
+    y, g = _run(inp, segments=5)
+    yr, gr = _oracle(inp)
+    _close("y", y, yr)
+    for k in ("u", "dt", "A", "B", "C"):
+        _close(f"d{k}", g[k], gr[k])
+
+
+def test_forced_segments_bf16():
+    inp = make_inputs(2, 512, 64, 16, seed=8)
+    bf = {k: (torch.from_numpy(v).to(torch.bfloat16).float().numpy().astype(np.float64)
+              if k in ("u", "dt", "B", "C", "z", "g") else v) for k, v in inp.items()}
+    y, g = _run(bf, ("skip", "gate"), dtype=torch.bfloat16, segments=6)
+    yr, gr = _oracle(bf, ("skip", "gate"))
+    at = lambda r: 2e-2 * max(1.0, float(np.abs(r).max()))
+    _close("y", y, yr, 2e-2, at(yr))
+    for k in ("u", "dt", "A", "B", "C", "D", "z"):
+        _close(f"d{k}", g[k], gr[k], 2e-2, at(gr[k]))
+
+
+def test_automatic_split_of_a_long_row():
+    from selectssm_amd import _lib as L
+
+    shape = (1, 16384, 64, 16)
+    d = L.make_desc(*shape)
+    # 1 x 2 channel blocks x 4 waves: split into 512-step segments
+    assert L.size_query(L.lib().ssm_fwd_workspace_bytes, d) == 32 * 17 * 64 * 4
+    inp = make_inputs(*shape, seed=2)
+    y, g = _run(inp)
+    yr, gr = _oracle(inp)
+    _close("y", y, yr)
+    for k in ("u", "dt", "A", "B", "C"):
+        _close(f"d{k}", g[k], gr[k])
+
+
+def test_split_and_unsplit_agree():
+    inp = make_inputs(2, 4096, 96, 16, seed=4)
+    y1, g1 = _run(inp, ("skip", "gate"), segments=1)
+    y2, g2 = _run(inp, ("skip", "gate"), segments=16)
+    _close("y", y2, y1.detach().double().cpu().numpy())
+    for k in ("u", "dt", "A", "B", "C", "D", "z"):
+        _close(f"d{k}", g2[k], g1[k].double().cpu().numpy())
+
+
+# ------------------------------------------------------------ config 3 shape
+
+SHAPE3 = (1, 1 << 20, 1024, 16)
+
+
+@pytest.fixture(scope="module")
+def inputs3():
+    from selectssm_amd.synthetic import make_inputs_gpu
+
+    return make_inputs_gpu(*SHAPE3, seed=9)
+
+
+@pytest.fixture(scope="module")
+def split3(inputs3):
+    from selectssm_amd.scan import scan_bwd, scan_fwd
+
+    x = inputs3
+    y, ck = scan_fwd(x["u"], x["dt"], x["A"], x["B"], x["C"])
+    g = scan_bwd(x["u"], x["dt"], x["A"], x["B"], x["C"], None, None, ck, x["g"])
+    torch.cuda.synchronize()
+    return y, g
+
+
+def test_config3_split_is_automatic():
+    from selectssm_amd import _lib as L
+
+    d = L.make_desc(*SHAPE3)
+    assert L.size_query(L.lib().ssm_fwd_workspace_bytes, d) == 16 * 17 * 1024 * 4
+
+
+def test_config3_exact_linearity(inputs3, split3):
+    from selectssm_amd.scan import scan_bwd, scan_fwd
+
+    x = inputs3
+    y1, g1 = split3
+    assert torch.isfinite(y1).all()
+    y2, ck2 = scan_fwd(2 * x["u"], x["dt"], x["A"], x["B"], x["C"])
+    assert torch.equal(y2, 2 * y1)
+    del y2, ck2
+    _, ck = scan_fwd(x["u"], x["dt"], x["A"], x["B"], x["C"])
+    g2 = scan_bwd(x["u"], x["dt"], x["A"], x["B"], x["C"], None, None, ck, 2 * x["g"])
+    for a, b in zip(g1[:5], g2[:5]):
+        assert torch.isfinite(a).all()
+        assert torch.equal(b, 2 * a)
+
+
+def test_config3_split_matches_unsplit(inputs3, split3):
+    from selectssm_amd.scan import scan_bwd, scan_fwd
+
+    x = inputs3
+    y, g = split3
+    y1, ck1 = scan_fwd(x["u"], x["dt"], x["A"], x["B"], x["C"], segments=1)
+    _close("y", y, y1.double().cpu().numpy())
+    del y1
+    g1 = scan_bwd(x["u"], x["dt"], x["A"], x["B"], x["C"], None, None, ck1, x["g"], segments=1)
+    for name, a, b in zip(("du", "ddt", "dA", "dB", "dC"), g[:5], g1[:5]):
+        print(name, float((a - b).abs().max()), float(b.abs().max()), flush=True)
+        _close(name, a, b.double().cpu().numpy())
+
+
+def test_config3_channels_match_c_port(inputs3, split3):
+    from oracle import c_oracle
+
+    x = inputs3
+    y, g = split3
+    L_ = SHAPE3[1]
+    for lo in (0, SHAPE3[2] - 16):
+        sl = slice(lo, lo + 16)
+        h = {k: x[k][..., sl].contiguous().cpu().numpy() for k in ("u", "dt", "g")}
+        A = x["A"][sl].contiguous().cpu().numpy()
+        Bc = x["B"].cpu().numpy()
+        Cc = x["C"].cpu().numpy()
+        # channels are independent for y, du, ddelta and dA
+        yr = c_oracle.scan_fwd(h["u"], h["dt"], A, Bc, Cc, min_recursion_length=L_, nthreads=16, precision="f64")
+        gr = c_oracle.scan_bwd(h["u"], h["dt"], A, Bc, Cc, h["g"], min_recursion_length=L_, nthreads=16,
+                               precision="f64")
+        _close(f"y[{lo}]", y[..., sl], yr)
+        _close(f"du[{lo}]", g[0][..., sl], gr[0])
+        _close(f"ddt[{lo}]", g[1][..., sl], gr[1])
+        _close(f"dA[{lo}]", g[2][sl], gr[2])

@@ -316,3 +316,21 @@ def test_c_port_matches_numpy_oracle(shape, ml, sp):
     ref = O.scan_backward(*args, x["g"])
     for a, r, name in zip(got, ref, ("du", "ddt", "dA", "dB", "dC")):
         np.testing.assert_allclose(a, r, rtol=1e-4, atol=1e-5, err_msg=name)
+
+
+@pytest.mark.parametrize("shape,ml,sp", [((2, 96, 8, 4), 2, 2), ((2, 1000, 16, 16), 1000, 2), ((1, 64, 5, 3), 3, 4),
+                                         ((3, 37, 9, 16), 2, 2)])
+def test_c_port_f64_matches_numpy_oracle(shape, ml, sp):
+    """The float64 build of the C port agrees with the fp64 numpy restatement
+    to fp64 rounding (used as the oracle at sizes numpy cannot reach)."""
+    from oracle import c_oracle
+
+    x = make_inputs(*shape, seed=1)
+    args = (x["u"], x["dt"], x["A"], x["B"], x["C"])
+    y = c_oracle.scan_fwd(*args, ml, sp, nthreads=2, precision="f64")
+    assert y.dtype == np.float64
+    np.testing.assert_allclose(y, O.scan_forward(*args), rtol=1e-11, atol=1e-13)
+    got = c_oracle.scan_bwd(*args, x["g"], ml, sp, nthreads=2, precision="f64")
+    ref = O.scan_backward(*args, x["g"])
+    for a, r, name in zip(got, ref, ("du", "ddt", "dA", "dB", "dC")):
+        np.testing.assert_allclose(a, r, rtol=1e-10, atol=1e-12, err_msg=name)
