@@ -27,13 +27,29 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, REPO)
 
 HBM_PEAK_GBS = 8000.0
-CONFIG = dict(batch=8, seqlen=8192, dim=2048, dstate=16)
+
+# BASELINE.json configs at the op level (the scan's own shapes: D = D_inner).
+# --config 1 is the bench line; the others are extra measurements.
+CONFIGS = {
+    1: dict(batch=8, seqlen=8192, dim=2048, dstate=16, io="f32", directions=1,
+            workload="SelectiveSSM custom_vjp_scan selective scan fwd+bwd (configs[1])"),
+    2: dict(batch=4, seqlen=131072, dim=512, dstate=16, io="f32", directions=2,
+            workload="BidirectionalMamba scans fwd+bwd, forward and reverse+complement directions (configs[2])"),
+    3: dict(batch=1, seqlen=1 << 20, dim=1024, dstate=16, io="f32", directions=1,
+            workload="SelectiveSSM recursive_scan selective scan fwd+bwd, long sequence (configs[3])"),
+    4: dict(batch=16, seqlen=4096, dim=5120, dstate=16, io="bf16", directions=1,
+            workload="SelectiveSSM selective scan fwd+bwd, bf16 I/O, fp32 state (configs[4])"),
+}
+CONFIG = CONFIGS[1]
 
 
-def alg_bytes(B, L, D, N, w=4):
+def alg_bytes(B, L, D, N, w=4, gate=False):
     """Compulsory op-boundary bytes: every input read once, every output written once."""
     fwd = (3 * B * L * D + 2 * B * L * N) * w + 4 * D * N            # u, dt, y; B, C; A
     bwd = (5 * B * L * D + 4 * B * L * N) * w + 8 * D * N            # u, dt, dy, du, ddt; B, C, dB, dC; A, dA
+    if gate:
+        fwd += B * L * D * w                                          # z
+        bwd += 2 * B * L * D * w                                      # z, dz
     return fwd, bwd
 
 
@@ -87,6 +103,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--config", type=int, default=1, choices=sorted(CONFIGS),
+                    help="BASELINE.json config to run (1 is the bench line)")
+    ap.add_argument("--gate", action="store_true", help="fuse the silu(z) gate (BidirectionalMamba epilogue)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (known HBM bytes) to scale rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE counters")
@@ -112,38 +131,59 @@ def main():
     from selectssm_amd.scan import scan_bwd, scan_fwd
     from selectssm_amd.synthetic import make_inputs_gpu
 
-    B, L, D, N = CONFIG["batch"], CONFIG["seqlen"], CONFIG["dim"], CONFIG["dstate"]
+    cfg = CONFIGS[args.config]
+    B, L, D, N = cfg["batch"], cfg["seqlen"], cfg["dim"], cfg["dstate"]
+    io = torch.bfloat16 if cfg["io"] == "bf16" else torch.float32
+    w = 2 if cfg["io"] == "bf16" else 4
     x = make_inputs_gpu(B, L, D, N, seed=0)
-    u, dt, A, Bc, Cc, g = x["u"], x["dt"], x["A"], x["B"], x["C"], x["g"]
+    u, dt, Bc, Cc, g = (x[k].to(io).contiguous() for k in ("u", "dt", "B", "C", "g"))
+    A = x["A"]
+    z = x["z"].to(io).contiguous() if args.gate else None
+    del x
+    # direction 2 is the reverse + complement scan with its own A
+    dirs = [dict(A=A, reverse=False, complement=False)]
+    if cfg["directions"] == 2:
+        dirs.append(dict(A=(A * 0.5).contiguous(), reverse=True, complement=True))
 
-    def step():
-        y, ckpt = scan_fwd(u, dt, A, Bc, Cc)
-        return scan_bwd(u, dt, A, Bc, Cc, None, None, ckpt, g)
+    def fwd(dr):
+        return scan_fwd(u, dt, dr["A"], Bc, Cc, None, z, dr["reverse"], dr["complement"])
+
+    def bwd(dr, ckpt):
+        return scan_bwd(u, dt, dr["A"], Bc, Cc, None, z, ckpt, g, dr["reverse"], dr["complement"])
 
     for _ in range(args.warmup):
-        step()
+        for dr in dirs:
+            bwd(dr, fwd(dr)[1])
     torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
 
     K = args.steps
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(K)]
+    nd = len(dirs)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3 * nd)] for _ in range(K)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for k in range(K):
-        ev[k][0].record()
-        y, ckpt = scan_fwd(u, dt, A, Bc, Cc)
-        ev[k][1].record()
-        scan_bwd(u, dt, A, Bc, Cc, None, None, ckpt, g)
-        ev[k][2].record()
+        for i, dr in enumerate(dirs):
+            ev[k][3 * i].record()
+            y, ckpt = fwd(dr)
+            ev[k][3 * i + 1].record()
+            bwd(dr, ckpt)
+            ev[k][3 * i + 2].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
 
-    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / K
-    bwd_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / K
-    fwd_b, bwd_b = alg_bytes(B, L, D, N)
+    fwd_ms = sum(e[3 * i].elapsed_time(e[3 * i + 1]) for e in ev for i in range(nd)) / (K * nd)
+    bwd_ms = sum(e[3 * i + 1].elapsed_time(e[3 * i + 2]) for e in ev for i in range(nd)) / (K * nd)
+    fwd_b, bwd_b = alg_bytes(B, L, D, N, w, gate=args.gate)
     tokens = B * L * K
     achieved = bwd_b / (bwd_ms * 1e-3) / 1e9
-    traffic = read_traffic(os.path.join(REPO, "profiles", "traffic_c1.txt"))
+    traffic = read_traffic(os.path.join(REPO, "profiles", "traffic_c1.txt")) if args.config == 1 and not args.gate \
+        else None
 
+    config = {"workload": cfg["workload"] + (" with the silu(z) gate fused" if args.gate else ""),
+              "batch": B, "seqlen": L, "d_inner": D, "d_state": N, "io": cfg["io"]}
+    if nd == 2:
+        config["directions"] = 2
     line = {
         "metric": "selective-scan fwd+bwd tokens/s and % of HBM roofline on 1 MI355X",
         "value": tokens / wall,
@@ -155,10 +195,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic (BASELINE.json configs[1] distributions, torch generator, seed 0)",
-        "config": {"workload": "SelectiveSSM custom_vjp_scan selective scan fwd+bwd (configs[1])",
-                   "batch": B, "seqlen": L, "d_inner": D, "d_state": N, "io": "f32"},
+        "dtype": "f32" if cfg["io"] == "f32" else "bf16 I/O, f32 state",
+        "data": f"synthetic (BASELINE.json configs[{args.config}] distributions, torch generator, seed 0)",
+        "config": config,
         "roofline": {
             "bound": "hbm",
             "kernel": "ssm_bwd (ssm_bwd_kernel + partial-sum reductions)",
@@ -170,11 +209,12 @@ def main():
             "alg_bytes_per_launch": bwd_b,
             "mean_launch_ms": bwd_ms,
         },
-        "step_roofline_frac": (fwd_b + bwd_b) / (wall / K) / 1e9 / HBM_PEAK_GBS,
+        "step_roofline_frac": nd * (fwd_b + bwd_b) / (wall / K) / 1e9 / HBM_PEAK_GBS,
         "fwd": {"mean_launch_ms": fwd_ms, "alg_bytes_per_launch": fwd_b,
                 "achieved_GBs": fwd_b / (fwd_ms * 1e-3) / 1e9},
+        "peak_hbm_bytes": torch.cuda.max_memory_allocated(),
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and args.config == 1 and not args.gate:
         line["cpu_baseline"] = cpu_baseline(B, L, D, N)
     print(json.dumps(line), flush=True)
 
