@@ -46,6 +46,9 @@ extern "C" {
 #define SSM_COMPLEMENT 2u /* with REVERSE: channel also mirrored, D-1-d (rcps.py:10-13) */
 #define SSM_SKIP 4u       /* y += u*Dskip with u in the scan domain (selectssm.py:238) */
 #define SSM_GATE 8u       /* y *= silu(z) (BidirectionalMamba, selectssm.py:335-336) */
+#define SSM_DELTA_SOFTPLUS 16u /* delta holds the pre-activation: the scan uses softplus(delta)
+                                  (selectssm.py:210) and ssm_bwd's ddelta is the gradient with
+                                  respect to that pre-activation */
 
 typedef struct ssm_desc {
   int64_t batch;          /* B */
@@ -53,7 +56,7 @@ typedef struct ssm_desc {
   int64_t dim;            /* D (channels, D_inner) */
   int64_t dstate;         /* N, 1..32 */
   int32_t dtype;          /* SSM_F32 or SSM_BF16 for u, delta, Bc, Cc, z, y, dy, du, ddelta, dB, dC, dz */
-  uint32_t flags;         /* SSM_REVERSE | SSM_COMPLEMENT | SSM_SKIP | SSM_GATE */
+  uint32_t flags;         /* SSM_REVERSE | SSM_COMPLEMENT | SSM_SKIP | SSM_GATE | SSM_DELTA_SOFTPLUS */
   int32_t delta_broadcast;/* 1: delta is (B,L,1) and shared by all channels */
   int32_t segments;       /* time segments per row: 0 = chosen from the shape, else 1..1024
                              (a row's time axis is split into this many segments that run
@@ -113,6 +116,55 @@ int ssm_bwd(void* stream, const ssm_desc_t* desc,
             const float* ckpt, const void* dy,
             void* du, void* ddelta, float* dA, void* dB, void* dC,
             float* dD, void* dz, void* workspace);
+
+/* ------------------------------------------------------------------------
+ * Causal depthwise conv1d + activation: the step before the scan
+ * (SelectiveSSM.__call__, selectssm.py:167-185).
+ *   u[b,t,d] = act( sum_k w[k,d] * x_s[b, t-(K-1)+k, d] ),  x_s[b,t,d] = 0 for t < 0
+ * where x_s is x seen in the scan domain: x itself, or with SSM_REVERSE the
+ * time-reversed x (x_s[b,t,d] = x[b,L-1-t,d]) and with SSM_COMPLEMENT also the
+ * channel-reversed x (x[b,L-1-t,D-1-d]), read through index maps rather than
+ * materialised flips (selectssm.py:167-168).  u is written in the scan domain,
+ * as the reference's u is; w (K,D) is the Flax kernel (K,1,D) of shift_conv,
+ * indexed by scan-domain channel.
+ * ------------------------------------------------------------------------ */
+
+/* conv activation (SelectiveSSM.activation, selectssm.py:176-185) */
+#define SSM_ACT_NONE 0
+#define SSM_ACT_SILU 1
+#define SSM_ACT_RELU 2
+
+typedef struct ssm_conv_desc {
+  int64_t batch;          /* B */
+  int64_t seqlen;         /* L */
+  int64_t dim;            /* D */
+  int32_t ksize;          /* K (shift_conv_size), 1..8 */
+  int32_t dtype;          /* SSM_F32 or SSM_BF16 for x, u, du, dx; w and dw are f32 */
+  uint32_t flags;         /* SSM_REVERSE | SSM_COMPLEMENT */
+  int32_t activation;     /* SSM_ACT_* */
+} ssm_conv_desc_t;
+
+/* Bytes of scratch `workspace` that ssm_conv_bwd needs (per-tile dw partial
+ * sums).  Returns 0 for an invalid desc. */
+size_t ssm_conv_bwd_workspace_bytes(const ssm_conv_desc_t* desc);
+
+/*
+ * u (B,L,D) = act(conv(x_s, w)) in the scan domain.
+ * Replaces: the flip, nn.Conv(feature_group_count=D, padding=[(K-1,0)],
+ * use_bias=False) and the activation of SelectiveSSM.__call__
+ * (selectssm.py:167-185).
+ */
+int ssm_conv_fwd(void* stream, const ssm_conv_desc_t* desc, const void* x, const float* w, void* u);
+
+/*
+ * Backward of ssm_conv_fwd for upstream gradient du (scan domain, like u):
+ * dx (B,L,D, the original domain of x) and dw (K,D).  The pre-activation is
+ * recomputed from x and w.  dx may be NULL (not written); dw may be NULL (then
+ * workspace may be NULL too).  Deterministic.
+ * Replaces: the autodiff of selectssm.py:167-185.
+ */
+int ssm_conv_bwd(void* stream, const ssm_conv_desc_t* desc, const void* x, const float* w, const void* du,
+                 void* dx, float* dw, void* workspace);
 
 #ifdef __cplusplus
 }

@@ -27,6 +27,8 @@ Pinning (what checks each function, in ``tests/test_oracle.py``):
   recursive_scan_backward == scan_backward for many (min_len, split)
   largest_factor_up_to    brute-force definition for all L <= 600, K <= 8
   causal_conv1d(_bwd)     numpy.convolve per channel; finite differences
+  conv_act_forward/_bwd   explicit np.flip composition, relu/silu closed forms;
+                          finite differences
   ssm_block_forward/_bwd  explicit np.flip composition; finite differences
 """
 from __future__ import annotations
@@ -166,6 +168,16 @@ def silu_grad(x):
     return s * (1.0 + x * (1.0 - s))
 
 
+def softplus(x):
+    """log(1 + e^x) in fp64 (selectssm.py:210, jax.nn.softplus = logaddexp(x, 0))."""
+    return np.logaddexp(np.asarray(x, np.float64), 0.0)
+
+
+def sigmoid(x):
+    """softplus'(x)."""
+    return 1.0 / (1.0 + np.exp(-np.asarray(x, np.float64)))
+
+
 def flip_domain(x, complement: bool):
     """Reverse map of ``SelectiveSSM(reverse=True)`` (selectssm.py:168, 231).
 
@@ -175,7 +187,8 @@ def flip_domain(x, complement: bool):
     return np.flip(x, axis=(-2, -1) if complement else -2)
 
 
-def ssm_block_forward(u, delta, A, B, C, Dskip=None, z=None, reverse=False, complement=False):
+def ssm_block_forward(u, delta, A, B, C, Dskip=None, z=None, reverse=False, complement=False,
+                      delta_softplus=False):
     """Scan + the scan-adjacent epilogue of ``SelectiveSSM``/``BidirectionalMamba``.
 
     u, delta, B, C are in the scan domain (already flipped when reverse=True,
@@ -184,7 +197,11 @@ def ssm_block_forward(u, delta, A, B, C, Dskip=None, z=None, reverse=False, comp
       y = flip(y) if reverse                          (selectssm.py:230-231)
       y = y + u * D      u NOT un-flipped (quirk)     (selectssm.py:238)
       y = y * silu(z)    BidirectionalMamba gate      (selectssm.py:335-336)
+    delta_softplus: ``delta`` is the pre-activation, the scan uses softplus(delta)
+    (selectssm.py:210).
     """
+    if delta_softplus:
+        delta = softplus(delta)
     y = scan_forward(u, delta, A, B, C)
     if reverse:
         y = flip_domain(y, complement)
@@ -195,11 +212,17 @@ def ssm_block_forward(u, delta, A, B, C, Dskip=None, z=None, reverse=False, comp
     return y
 
 
-def ssm_block_backward(u, delta, A, B, C, dout, Dskip=None, z=None, reverse=False, complement=False):
+def ssm_block_backward(u, delta, A, B, C, dout, Dskip=None, z=None, reverse=False, complement=False,
+                       delta_softplus=False):
     """Chain rule through ``ssm_block_forward`` in fp64.
 
     Returns (du, ddelta, dA, dB, dC, dD, dz); dD / dz are None when unused.
+    With delta_softplus, ddelta is w.r.t. the pre-activation (times sigmoid).
     """
+    dsig = None
+    if delta_softplus:
+        dsig = sigmoid(delta)
+        delta = softplus(delta)
     u64 = np.asarray(u, np.float64)
     dout = np.asarray(dout, np.float64)
     dz = None
@@ -220,6 +243,8 @@ def ssm_block_backward(u, delta, A, B, C, dout, Dskip=None, z=None, reverse=Fals
         du_skip = dy * np.asarray(Dskip, np.float64)
     dys = flip_domain(dy, complement) if reverse else dy
     du, ddt, dA, dB, dC = scan_backward(u, delta, A, B, C, dys)
+    if dsig is not None:
+        ddt = ddt * dsig
     return du + du_skip, ddt, dA, dB, dC, dD, dz
 
 
@@ -267,6 +292,45 @@ def conv1d_silu_backward(x, w, du):
     v = causal_conv1d(x, w)
     dv = np.asarray(du, np.float64) * silu_grad(v)
     return causal_conv1d_backward(x, w, dv)
+
+
+def activate(x, activation):
+    """SelectiveSSM's activation after the conv (selectssm.py:176-185): silu, relu or none."""
+    x = np.asarray(x, np.float64)
+    if activation == "silu":
+        return silu(x)
+    if activation == "relu":
+        return np.maximum(x, 0.0)
+    if activation is None or activation == "none":
+        return x
+    raise ValueError(activation)
+
+
+def activate_grad(x, activation):
+    """d activate / dx; relu'(0) = 0 as jax.nn.relu's gradient."""
+    x = np.asarray(x, np.float64)
+    if activation == "silu":
+        return silu_grad(x)
+    if activation == "relu":
+        return (x > 0).astype(np.float64)
+    return np.ones_like(x)
+
+
+def conv_act_forward(x, w, activation="silu", reverse=False, complement=False):
+    """SelectiveSSM's flip -> shift_conv -> activation (selectssm.py:167-185).
+
+    x in its original domain; the result u is in the scan domain.
+    """
+    xs = flip_domain(x, complement) if reverse else np.asarray(x, np.float64)
+    return activate(causal_conv1d(xs, w), activation)
+
+
+def conv_act_backward(x, w, du, activation="silu", reverse=False, complement=False):
+    """(dx, dw) of ``conv_act_forward``; dx in x's domain."""
+    xs = flip_domain(x, complement) if reverse else np.asarray(x, np.float64)
+    dv = np.asarray(du, np.float64) * activate_grad(causal_conv1d(xs, w), activation)
+    dxs, dw = causal_conv1d_backward(xs, w, dv)
+    return (flip_domain(dxs, complement) if reverse else dxs), dw
 
 
 # --------------------------------------------------------------------------

@@ -2,9 +2,11 @@
 
 The hot path of ``selectssm`` (the selective scan y = scan(u, dt, A, B, C) with
 its custom-VJP backward, plus the scan-adjacent epilogue of ``SelectiveSSM`` /
-``BidirectionalMamba``) runs as hand-written HIP kernels exported through the C
-ABI in ``include/selectssm.h``.  There is no CPU fallback.
+``BidirectionalMamba`` and the causal conv + activation before the scan) runs as
+hand-written HIP kernels exported through the C ABI in ``include/selectssm.h``.
+There is no CPU fallback.
 """
+from .conv import conv1d_act
 from .scan import (
     SelectiveScanFn,
     largest_factor_up_to,
@@ -17,6 +19,7 @@ from .scan import (
 
 __all__ = [
     "SelectiveScanFn",
+    "conv1d_act",
     "largest_factor_up_to",
     "resolve_chunking",
     "selective_scan",

@@ -22,6 +22,11 @@ SSM_REVERSE = 1
 SSM_COMPLEMENT = 2
 SSM_SKIP = 4
 SSM_GATE = 8
+SSM_DELTA_SOFTPLUS = 16
+
+SSM_ACT_NONE = 0
+SSM_ACT_SILU = 1
+SSM_ACT_RELU = 2
 
 ABI_VERSION = 2
 
@@ -34,6 +39,9 @@ EXPORTS = (
     "ssm_bwd_workspace_bytes",
     "ssm_fwd",
     "ssm_bwd",
+    "ssm_conv_bwd_workspace_bytes",
+    "ssm_conv_fwd",
+    "ssm_conv_bwd",
 )
 
 
@@ -49,6 +57,20 @@ class SsmDesc(ctypes.Structure):
         ("flags", ctypes.c_uint32),
         ("delta_broadcast", ctypes.c_int32),
         ("segments", ctypes.c_int32),
+    ]
+
+
+class SsmConvDesc(ctypes.Structure):
+    """Mirror of ``ssm_conv_desc_t``."""
+
+    _fields_ = [
+        ("batch", ctypes.c_int64),
+        ("seqlen", ctypes.c_int64),
+        ("dim", ctypes.c_int64),
+        ("ksize", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("flags", ctypes.c_uint32),
+        ("activation", ctypes.c_int32),
     ]
 
 
@@ -81,6 +103,13 @@ def _declare(lib):
     lib.ssm_fwd.argtypes = [vp, dp, vp, vp, fp, vp, vp, fp, vp, vp, fp, vp]
     lib.ssm_bwd.restype = ctypes.c_int
     lib.ssm_bwd.argtypes = [vp, dp, vp, vp, fp, vp, vp, fp, vp, fp, vp, vp, vp, fp, vp, vp, fp, vp, vp]
+    cp = ctypes.POINTER(SsmConvDesc)
+    lib.ssm_conv_bwd_workspace_bytes.restype = ctypes.c_size_t
+    lib.ssm_conv_bwd_workspace_bytes.argtypes = [cp]
+    lib.ssm_conv_fwd.restype = ctypes.c_int
+    lib.ssm_conv_fwd.argtypes = [vp, cp, vp, fp, vp]
+    lib.ssm_conv_bwd.restype = ctypes.c_int
+    lib.ssm_conv_bwd.argtypes = [vp, cp, vp, fp, vp, vp, fp, vp]
 
 
 def lib():

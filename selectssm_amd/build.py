@@ -1,6 +1,7 @@
 """Build recipe for the in-tree HIP library ``selectssm_amd/libselectssm.so``.
 
-One translation unit, compiled for gfx950 with hipcc.  Packed-FP32 VALU
+The scan (csrc/selectssm.hip) and the causal conv (csrc/conv.hip), compiled
+for gfx950 with hipcc into one shared library.  Packed-FP32 VALU
 instructions are disabled for all device code (``-packed-fp32-ops``).
 Run ``python -m selectssm_amd.build`` or call :func:`build`.
 """
@@ -13,7 +14,7 @@ import sys
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
-SRC = os.path.join(PKG_DIR, "csrc", "selectssm.hip")
+SRCS = [os.path.join(PKG_DIR, "csrc", f) for f in ("selectssm.hip", "conv.hip")]
 LIB = os.path.join(PKG_DIR, "libselectssm.so")
 ARCH = "gfx950"
 
@@ -38,7 +39,7 @@ def hipcc_path() -> str:
 def build(verbose: bool = False) -> str:
     """Compile ``libselectssm.so`` (always recompiles).  Returns its path."""
     tmp = LIB + ".tmp"
-    cmd = [hipcc_path(), *HIPCC_FLAGS, "-o", tmp, SRC]
+    cmd = [hipcc_path(), *HIPCC_FLAGS, "-o", tmp, *SRCS]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -1,0 +1,99 @@
+"""Causal depthwise conv1d + activation: the step before the scan.
+
+``conv1d_act`` is SelectiveSSM's flip -> ``shift_conv`` -> activation
+(selectssm.py:167-185) as one HIP kernel pair (``ssm_conv_fwd`` /
+``ssm_conv_bwd``).  The flip is an index map inside the kernels: x is given in
+its original domain, u comes back in the scan domain (the domain the scan and
+the Dense projections of SelectiveSSM see), and dx in x's domain.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib as L
+from .scan import _IO_DTYPES, _ptr, _scratch, _stream
+
+_ACTS = {None: L.SSM_ACT_NONE, "none": L.SSM_ACT_NONE, "silu": L.SSM_ACT_SILU, "relu": L.SSM_ACT_RELU}
+
+
+def _act_code(activation):
+    if activation not in _ACTS:
+        # the reference raises for an unknown activation name (selectssm.py:184-185)
+        raise Exception(f"Unknown activation: {activation}")
+    return _ACTS[activation]
+
+
+def _conv_desc(x, K, reverse, complement, activation):
+    Bt, Ln, D = x.shape
+    flags = 0
+    if reverse:
+        flags |= L.SSM_REVERSE
+        if complement:
+            flags |= L.SSM_COMPLEMENT
+    return L.SsmConvDesc(Bt, Ln, D, int(K), _IO_DTYPES[x.dtype], flags, _act_code(activation))
+
+
+def _weight(w, D):
+    w = w.reshape(w.shape[0], -1) if w.dim() == 3 else w  # Flax (K, 1, D) kernel
+    if w.dim() != 2 or w.shape[1] != D:
+        raise ValueError(f"conv kernel must be (K, D) or (K, 1, D) with D={D}, got {tuple(w.shape)}")
+    return w
+
+
+def conv_fwd(x, w, reverse=False, complement=False, activation="silu"):
+    """u = act(conv(x_s, w)) in the scan domain (``ssm_conv_fwd``)."""
+    desc = _conv_desc(x, w.shape[0], reverse, complement, activation)
+    u = torch.empty_like(x)
+    L.check(L.lib().ssm_conv_fwd(_stream(), ctypes.byref(desc), _ptr(x), _ptr(w), _ptr(u)))
+    return u
+
+
+def conv_bwd(x, w, du, reverse=False, complement=False, activation="silu", need_dx=True, need_dw=True):
+    """(dx, dw) of :func:`conv_fwd` (``ssm_conv_bwd``); either may be skipped (None)."""
+    desc = _conv_desc(x, w.shape[0], reverse, complement, activation)
+    lib = L.lib()
+    dx = torch.empty_like(x) if need_dx else None
+    dw = torch.empty_like(w) if need_dw else None
+    ws = _scratch(L.size_query(lib.ssm_conv_bwd_workspace_bytes, desc), x.device) if need_dw else None
+    L.check(lib.ssm_conv_bwd(_stream(), ctypes.byref(desc), _ptr(x), _ptr(w), _ptr(du), _ptr(dx), _ptr(dw),
+                             _ptr(ws)))
+    return dx, dw
+
+
+class ConvActFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, w, reverse, complement, activation):
+        ctx.save_for_backward(x, w)
+        ctx.cfg = (reverse, complement, activation)
+        return conv_fwd(x, w, reverse, complement, activation)
+
+    @staticmethod
+    def backward(ctx, du):
+        x, w = ctx.saved_tensors
+        dx, dw = conv_bwd(x, w, du.to(x.dtype).contiguous(), *ctx.cfg, need_dx=ctx.needs_input_grad[0],
+                          need_dw=ctx.needs_input_grad[1])
+        return dx, dw, None, None, None
+
+
+def conv1d_act(x, w, reverse=False, complement=False, activation="silu"):
+    """SelectiveSSM's flip + causal depthwise conv + activation (selectssm.py:167-185).
+
+    x: (B, L, D) float32 / bfloat16 GPU tensor in its original domain.
+    w: the ``shift_conv`` kernel, (K, 1, D) as Flax stores it, or (K, D); float32.
+    Returns u (B, L, D) in the scan domain: u[b,t,d] = act(sum_k w[k,d] x_s[b,t-(K-1)+k,d])
+    with x_s = x, or x flipped in time (and in channels with ``complement``) when
+    ``reverse``.  ``activation``: "silu" (the reference's default), "relu" or None.
+    """
+    if x.dim() != 3:
+        raise ValueError(f"x must be (B, L, D), got shape {tuple(x.shape)}")
+    if not (x.is_cuda and w.is_cuda):
+        raise ValueError("conv1d_act inputs must be GPU tensors (there is no CPU path)")
+    if x.dtype not in _IO_DTYPES:
+        raise TypeError(f"conv1d_act supports float32 and bfloat16 activations, got {x.dtype}")
+    if complement and not reverse:
+        complement = False  # the reference only looks at complement when reverse (selectssm.py:116, 167-168)
+    _act_code(activation)
+    w = _weight(w, x.shape[-1]).to(torch.float32).contiguous()
+    return ConvActFn.apply(x.contiguous(), w, bool(reverse), bool(complement), activation)

@@ -40,149 +40,18 @@
 #include <type_traits>
 
 #include "../../include/selectssm.h"
+#include "common.h"
 
 namespace {
 
-constexpr float kLog2e = 1.4426950408889634f;
+using namespace ssm;
+
 constexpr int kWave = 64;
 constexpr int kCh = 32;   // channels per workgroup (lane & 31)
 constexpr int kSPW = 4;   // states per wave: 2 per lane, the two lane halves differ
 constexpr int kTT = 32;   // forward time tile
 constexpr int kCK = 16;   // checkpoint interval = backward block length
 constexpr int kRB = 4;    // backward steps per batched dB / dC reduction (4 steps x 2 states)
-
-// ---------------------------------------------------------------- element I/O
-
-struct bf16 {
-  uint16_t bits;
-};
-
-template <typename T>
-__device__ __forceinline__ float ld(const T* p, int64_t i);
-template <>
-__device__ __forceinline__ float ld<float>(const float* p, int64_t i) {
-  return p[i];
-}
-template <>
-__device__ __forceinline__ float ld<bf16>(const bf16* p, int64_t i) {
-  return __uint_as_float(static_cast<uint32_t>(p[i].bits) << 16);
-}
-
-// Element `off` of a (wave-uniform) base pointer, addressed with a 32-bit byte
-// offset so the load is one SGPR-base + VGPR-offset instruction (the host
-// keeps every per-batch-row byte offset below 2^32).
-template <typename T>
-__device__ __forceinline__ float ld32(const T* base, uint32_t off) {
-  const uint32_t byte = off * (uint32_t)sizeof(T);
-  return ld(reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + byte), 0);
-}
-
-template <typename T>
-__device__ __forceinline__ void st(T* p, int64_t i, float v);
-template <>
-__device__ __forceinline__ void st<float>(float* p, int64_t i, float v) {
-  p[i] = v;
-}
-template <>
-__device__ __forceinline__ void st<bf16>(bf16* p, int64_t i, float v) {
-  // round to nearest even; NaN stays a quiet NaN
-  uint32_t x = __float_as_uint(v);
-  uint16_t r;
-  if ((x & 0x7fffffffu) > 0x7f800000u) {
-    r = static_cast<uint16_t>((x >> 16) | 0x40u);
-  } else {
-    x += 0x7fffu + ((x >> 16) & 1u);
-    r = static_cast<uint16_t>(x >> 16);
-  }
-  p[i].bits = r;
-}
-
-// store counterpart of ld32
-template <typename T>
-__device__ __forceinline__ void st32(T* base, uint32_t off, float v) {
-  const uint32_t byte = off * (uint32_t)sizeof(T);
-  st(reinterpret_cast<T*>(reinterpret_cast<char*>(base) + byte), 0, v);
-}
-
-// Runs f() on the lanes whose channel exists.  A workgroup whose 64 channels
-// all exist (every one when D % 64 == 0) takes a wave-uniform branch and needs
-// no per-lane exec masking.
-template <typename F>
-__device__ __forceinline__ void on_valid_lanes(bool full_block, bool valid, F&& f) {
-  if (full_block) {
-    f();
-  } else if (valid) {
-    f();
-  }
-}
-
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-__device__ __forceinline__ float sigmoid(float x) {
-  return 1.0f / (1.0f + fast_exp2(-x * kLog2e));
-}
-
-// ------------------------------------------------------ cross-lane reductions
-
-template <int CTRL>
-__device__ __forceinline__ float dpp_move(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
-}
-
-// Sum of v over the 16 lanes of each row; every lane of the row gets it.
-__device__ __forceinline__ float row_sum16(float v) {
-  v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]
-  v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]
-  v += dpp_move<0x141>(v);  // row_half_mirror
-  v += dpp_move<0x140>(v);  // row_mirror
-  return v;
-}
-
-// Sum of v over the 32 lanes of each wave half; every lane of the half gets it.
-__device__ __forceinline__ float half_sum32(float v) {
-  v = row_sum16(v);
-  auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-}
-
-// Lanes l and l^32 hold the two halves of one channel's sum: the result is a
-// summed over the halves in lanes < 32 and b summed over the halves in lanes >= 32.
-__device__ __forceinline__ float half_pair(float a, float b) {
-  auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
-  return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-}
-
-// Eight per-lane values, each summed over the 32 lanes of its wave half: 16
-// totals per wave.  Lane l ends with the total of x[reduce32x8_value(l)] over
-// half reduce32x8_half(l); the 4 lanes of each aligned quad hold the same one.
-__device__ __forceinline__ float reduce32x8(const float (&x)[8]) {
-  float p[4];
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {  // rows 0..3 keep x[2m], x[2m+1] of half 0, x[2m], x[2m+1] of half 1
-    auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(x[2 * m]), __float_as_uint(x[2 * m + 1]), false, false);
-    p[m] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-  }
-  const int lid = __lane_id();
-  const bool b3 = (lid & 8) != 0;
-  const bool b2 = (lid & 4) != 0;
-  float q[2];
-#pragma unroll
-  for (int m = 0; m < 2; ++m) {  // lanes with bit 3 clear keep p[2m], set keep p[2m+1]
-    const float keep = b3 ? p[2 * m + 1] : p[2 * m];
-    const float give = b3 ? p[2 * m] : p[2 * m + 1];
-    q[m] = keep + dpp_move<0x128>(give);  // row_ror:8
-  }
-  const float keep = b2 ? q[1] : q[0];    // bit 2 clear keeps q[0], set keeps q[1]
-  const float give = b2 ? q[0] : q[1];
-  float r = keep + dpp_move<0x141>(give);  // row_half_mirror
-  r += dpp_move<0xB1>(r);                  // quad_perm [1,0,3,2]
-  r += dpp_move<0x4E>(r);                  // quad_perm [2,3,0,1]
-  return r;
-}
-__device__ __forceinline__ int reduce32x8_value(int lane) {
-  return 4 * ((lane >> 2) & 1) + 2 * ((lane >> 3) & 1) + ((lane >> 4) & 1);
-}
-__device__ __forceinline__ int reduce32x8_half(int lane) { return lane >> 5; }
 
 // --------------------------------------------------------------- forward
 
@@ -246,6 +115,7 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kerne
   const bool skip = EPI && (p.flags & SSM_SKIP);
   const bool gate = EPI && (p.flags & SSM_GATE);
   const bool stage_eu = skip && rev;  // u at the output position is another element
+  const bool dsp = p.flags & SSM_DELTA_SOFTPLUS;
   // staging / output mapping: thread -> column scol, rows srow0 + k * RSTEP
   const int scol = tid & (kCh - 1);
   const int srow0 = tid / kCh;
@@ -343,7 +213,7 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kerne
       const int i = srow0 + k * RSTEP;
       const bool in = svalid && t0 + i < L;
       s_u[buf][i][scol] = in ? r_u[k] : 0.0f;
-      s_dt[buf][i][scol] = in ? r_dt[k] : 0.0f;
+      s_dt[buf][i][scol] = in ? (dsp ? softplus(r_dt[k]) : r_dt[k]) : 0.0f;
       if (stage_eu) s_eu[buf][i][scol] = in ? r_eu[k] : 0.0f;
       if (gate) s_ez[buf][i][scol] = in ? r_ez[k] : 0.0f;
     }
@@ -515,6 +385,7 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
   const bool skip = EPI && (p.flags & SSM_SKIP);
   const bool stage_dyo = skip && rev;         // gated dy at the unmirrored (t,d) for the skip term
   const bool stage_eu = gate && skip && rev;  // u at the output position for y_pre
+  const bool dsp = p.flags & SSM_DELTA_SOFTPLUS;
   const int scol = tid & (kCh - 1);
   const int srow0 = tid / kCh;
   const int sd = cb * kCh + scol;
@@ -565,6 +436,7 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
   __shared__ float s_eu[EB][ER][kCh], s_dyo[EB][ER][kCh];
   __shared__ __attribute__((aligned(16))) float s_B[2][kCK][NS];
   __shared__ __attribute__((aligned(16))) float s_C[2][kCK][NS];
+  __shared__ float s_sig[2][kCK][kCh];                 // softplus'(delta) = sigmoid(delta) (SSM_DELTA_SOFTPLUS)
   __shared__ float sbuf[EPI ? 2 : 1][NG][kCK][kWave];  // [du | ddelta] per wave; (gate) y per lane
   __shared__ float bcbuf[2][kCK][NS];                  // dB, dC totals of this channel block
   __shared__ float bdummy[2][kWave];                   // sink for lanes without a total
@@ -630,7 +502,12 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
       const int i = srow0 + k * RSTEP;
       const bool in = svalid && t0 + i < L;
       s_u[buf][i][scol] = in ? r_u[k] : 0.0f;
-      s_dt[buf][i][scol] = in ? r_dt[k] : 0.0f;
+      if (dsp) {
+        s_dt[buf][i][scol] = in ? softplus(r_dt[k]) : 0.0f;
+        s_sig[buf][i][scol] = in ? sigmoid(r_dt[k]) : 0.0f;
+      } else {
+        s_dt[buf][i][scol] = in ? r_dt[k] : 0.0f;
+      }
       const float go = in ? r_dy[k] : 0.0f;
       if (gate) {
         const float gz = in ? r_gz[k] : 0.0f;
@@ -778,6 +655,7 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
           }
           const int t = t0 + i;
           const float uu = s_u[buf][i][scol];
+          if (dsp) ddt *= s_sig[buf][i][scol];  // through softplus (the same factor for every channel when broadcast)
           if (skip) {
             // y_out[t,d] holds u[t,d]*D[d] (selectssm.py:238): its gradient lands on u[t,d]
             const float dyo = stage_dyo ? s_dyo[buf][i][scol] : s_dy[buf][i][scol];
@@ -886,6 +764,7 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_agg_k
   const bool rev = p.flags & SSM_REVERSE;
   const bool comp = rev && (p.flags & SSM_COMPLEMENT);
   const bool gate = EPI && (p.flags & SSM_GATE);
+  const bool dsp = p.flags & SSM_DELTA_SOFTPLUS;
   const int scol = tid & (kCh - 1);
   const int srow0 = tid / kCh;
   const int sd = cb * kCh + scol;
@@ -943,7 +822,7 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_agg_k
     for (int k = 0; k < RPT; ++k) {
       const int i = srow0 + k * RSTEP;
       const bool in = svalid && t0 + i < L;
-      s_dt[buf][i][scol] = in ? r_dt[k] : 0.0f;
+      s_dt[buf][i][scol] = in ? (dsp ? softplus(r_dt[k]) : r_dt[k]) : 0.0f;
       const float go = in ? r_dy[k] : 0.0f;
       if (gate) {
         const float gz = in ? r_gz[k] : 0.0f;
@@ -1013,18 +892,6 @@ __global__ void reduce_parts_kernel(const float* __restrict__ ws, TO* __restrict
 
 // ------------------------------------------------------------------- host side
 
-thread_local std::string g_last_error;
-
-int fail(int code, const std::string& msg) {
-  g_last_error = msg;
-  return code;
-}
-
-int hip_check(hipError_t e, const char* what) {
-  if (e != hipSuccess) return fail(SSM_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
-  return SSM_OK;
-}
-
 struct Shape {
   int B, L, D, N, nblk, ncb;
   int NG;    // waves per workgroup (4 states each)
@@ -1066,7 +933,7 @@ int validate(const ssm_desc_t* desc, Shape* s) {
   if ((desc->seqlen + kCK - 1) / kCK * desc->dstate * desc->dim > (int64_t(1) << 30))
     return fail(SSM_ERR_INVALID, "checkpoints of one batch row must hold <= 2^30 floats");
   if (desc->dtype != SSM_F32 && desc->dtype != SSM_BF16) return fail(SSM_ERR_INVALID, "dtype must be SSM_F32 or SSM_BF16");
-  if (desc->flags & ~(SSM_REVERSE | SSM_COMPLEMENT | SSM_SKIP | SSM_GATE))
+  if (desc->flags & ~(SSM_REVERSE | SSM_COMPLEMENT | SSM_SKIP | SSM_GATE | SSM_DELTA_SOFTPLUS))
     return fail(SSM_ERR_INVALID, "unknown flag bits");
   if ((desc->flags & SSM_COMPLEMENT) && !(desc->flags & SSM_REVERSE))
     return fail(SSM_ERR_INVALID, "SSM_COMPLEMENT requires SSM_REVERSE (selectssm.py:116)");
@@ -1230,6 +1097,22 @@ int launch_bwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const voi
 }  // namespace
 
 // ------------------------------------------------------------------- C ABI
+
+namespace ssm {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(SSM_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+  return SSM_OK;
+}
+
+}  // namespace ssm
 
 extern "C" {
 

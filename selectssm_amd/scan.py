@@ -96,8 +96,8 @@ def _stream():
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
-def _flags(skip, gate, reverse, complement):
-    f = 0
+def _flags(skip, gate, reverse, complement, delta_softplus=False):
+    f = L.SSM_DELTA_SOFTPLUS if delta_softplus else 0
     if reverse:
         f |= L.SSM_REVERSE
         if complement:
@@ -122,13 +122,15 @@ def _scratch(nbytes, device):
 # ------------------------------------------------------------- raw launchers
 
 def scan_fwd(u, delta, A, B, C, Dskip=None, z=None, reverse=False, complement=False, want_ckpt=True,
-             segments=0):
+             segments=0, delta_softplus=False):
     """Run ``ssm_fwd``.  All tensors contiguous, on one GPU, I/O dtype shared.
 
-    ``segments`` splits each row's time axis (0: chosen from the shape).
-    Returns ``(y, ckpt)``; ``ckpt`` is None when ``want_ckpt`` is False.
+    ``segments`` splits each row's time axis (0: chosen from the shape);
+    ``delta_softplus``: ``delta`` is the pre-activation and the scan uses
+    softplus(delta).  Returns ``(y, ckpt)``; ``ckpt`` is None when
+    ``want_ckpt`` is False.
     """
-    flags = _flags(Dskip is not None, z is not None, reverse, complement)
+    flags = _flags(Dskip is not None, z is not None, reverse, complement, delta_softplus)
     desc = _desc(u, delta, A, flags, segments)
     lib = L.lib()
     y = torch.empty_like(u)
@@ -139,9 +141,11 @@ def scan_fwd(u, delta, A, B, C, Dskip=None, z=None, reverse=False, complement=Fa
     return y, ckpt
 
 
-def scan_bwd(u, delta, A, B, C, Dskip, z, ckpt, dy, reverse=False, complement=False, segments=0):
-    """Run ``ssm_bwd``.  Returns ``(du, ddelta, dA, dB, dC, dD, dz)`` (dD / dz None when unused)."""
-    flags = _flags(Dskip is not None, z is not None, reverse, complement)
+def scan_bwd(u, delta, A, B, C, Dskip, z, ckpt, dy, reverse=False, complement=False, segments=0,
+             delta_softplus=False):
+    """Run ``ssm_bwd``.  Returns ``(du, ddelta, dA, dB, dC, dD, dz)`` (dD / dz None when unused);
+    with ``delta_softplus``, ``ddelta`` is the gradient w.r.t. the pre-activation."""
+    flags = _flags(Dskip is not None, z is not None, reverse, complement, delta_softplus)
     desc = _desc(u, delta, A, flags, segments)
     lib = L.lib()
     du = torch.empty_like(u)
@@ -169,12 +173,14 @@ class SelectiveScanFn(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, u, delta, A, B, C, Dskip, z, reverse, complement, segments=0):
+    def forward(ctx, u, delta, A, B, C, Dskip, z, reverse, complement, segments=0, delta_softplus=False):
         y, ckpt = scan_fwd(u, delta, A, B, C, Dskip, z, reverse, complement,
-                           want_ckpt=torch.is_grad_enabled() or any(ctx.needs_input_grad), segments=segments)
+                           want_ckpt=torch.is_grad_enabled() or any(ctx.needs_input_grad), segments=segments,
+                           delta_softplus=delta_softplus)
         ctx.save_for_backward(u, delta, A, B, C, Dskip, z, ckpt)
         ctx.flags = (reverse, complement)
         ctx.segments = segments
+        ctx.delta_softplus = delta_softplus
         return y
 
     @staticmethod
@@ -182,11 +188,12 @@ class SelectiveScanFn(torch.autograd.Function):
         u, delta, A, B, C, Dskip, z, ckpt = ctx.saved_tensors
         dy = dy.to(u.dtype).contiguous()
         du, ddelta, dA, dB, dC, dD, dz = scan_bwd(u, delta, A, B, C, Dskip, z, ckpt, dy, *ctx.flags,
-                                                  segments=ctx.segments)
-        return du, ddelta, dA, dB, dC, dD, dz, None, None, None
+                                                  segments=ctx.segments, delta_softplus=ctx.delta_softplus)
+        return du, ddelta, dA, dB, dC, dD, dz, None, None, None, None
 
 
-def selective_scan(u, delta, A, B, C, D=None, z=None, reverse=False, complement=False, segments=0):
+def selective_scan(u, delta, A, B, C, D=None, z=None, reverse=False, complement=False, segments=0,
+                   delta_softplus=False):
     """Fused selective scan with the SelectiveSSM / BidirectionalMamba epilogue.
 
     u, delta, B, C are in the scan domain (flipped already when ``reverse``,
@@ -197,6 +204,8 @@ def selective_scan(u, delta, A, B, C, D=None, z=None, reverse=False, complement=
         y = y + u * D          if D is given     (selectssm.py:238; u stays flipped)
         y = y * silu(z)        if z is given     (selectssm.py:335-336)
     ``complement`` (with ``reverse``) also mirrors the channel axis.
+    ``delta_softplus``: ``delta`` is the pre-activation of selectssm.py:210;
+    the scan uses softplus(delta) and the gradient flows to the pre-activation.
     ``segments`` > 0 forces that many time segments per row (0: the library
     splits rows only when there are too few to fill the GPU); the result
     agrees with one segment up to fp32 rounding.
@@ -210,7 +219,7 @@ def selective_scan(u, delta, A, B, C, D=None, z=None, reverse=False, complement=
     if not 0 <= int(segments) <= 1024:
         raise ValueError(f"segments must be in 0..1024, got {segments}")
     return SelectiveScanFn.apply(cast(u), cast(delta), fcast(A), cast(B), cast(C), fcast(D), cast(z),
-                                 bool(reverse), bool(complement), int(segments))
+                                 bool(reverse), bool(complement), int(segments), bool(delta_softplus))
 
 
 # ------------------------------------------------------- reference-named API

@@ -32,7 +32,8 @@ def test_header_constants_match_binding():
     text = open(HEADER).read()
     consts = dict(re.findall(r"#define (SSM_\w+) (\d+)u?", text))
     for k in ("SSM_OK", "SSM_ERR_INVALID", "SSM_ERR_UNSUPPORTED", "SSM_ERR_HIP", "SSM_F32", "SSM_BF16",
-              "SSM_REVERSE", "SSM_COMPLEMENT", "SSM_SKIP", "SSM_GATE"):
+              "SSM_REVERSE", "SSM_COMPLEMENT", "SSM_SKIP", "SSM_GATE", "SSM_DELTA_SOFTPLUS",
+              "SSM_ACT_NONE", "SSM_ACT_SILU", "SSM_ACT_RELU"):
         assert int(consts[k]) == getattr(L, k), k
     assert int(consts["SSM_ABI_VERSION"]) == L.ABI_VERSION
     assert ctypes.sizeof(L.SsmDesc) == 48
@@ -86,7 +87,7 @@ def test_split_forward_needs_its_workspace():
 
 @pytest.mark.parametrize("field,value,msg", [
     ("batch", 0, b"batch, seqlen and dim"), ("dstate", 0, b"dstate"), ("dtype", 7, b"dtype"),
-    ("flags", 64, b"unknown flag"), ("flags", 2, b"COMPLEMENT requires"), ("delta_broadcast", 3, b"delta_broadcast"),
+    ("flags", 32, b"unknown flag"), ("flags", 2, b"COMPLEMENT requires"), ("delta_broadcast", 3, b"delta_broadcast"),
     ("segments", -1, b"segments"), ("segments", 1025, b"segments"),
 ])
 def test_invalid_desc_is_rejected_before_any_launch(field, value, msg):
@@ -111,3 +112,22 @@ def test_null_pointers_and_missing_epilogue_operands_are_rejected():
     rc = lib.ssm_bwd(None, ctypes.byref(d), p, p, p, p, p, None, p, p, p, p, p, p, p, p, None, None, p)
     assert rc == L.SSM_ERR_INVALID and b"dz" in lib.ssm_last_error()
     assert lib.ssm_fwd(None, None, p, p, p, p, p, None, None, p, None, None) == L.SSM_ERR_INVALID
+
+
+def test_conv_desc_validation():
+    lib = L.lib()
+    assert ctypes.sizeof(L.SsmConvDesc) == 40
+    p = ctypes.c_void_p(16)
+    good = dict(batch=2, seqlen=64, dim=64, ksize=4, dtype=L.SSM_F32, flags=0, activation=L.SSM_ACT_SILU)
+    d = L.SsmConvDesc(**good)
+    # dw partial sums: one (K, D) slab per (batch row, 128-step tile)
+    assert lib.ssm_conv_bwd_workspace_bytes(ctypes.byref(d)) == 2 * 1 * 4 * 64 * 4
+    for field, value, msg in [("ksize", 0, b"ksize"), ("ksize", 9, b"ksize"), ("activation", 3, b"activation"),
+                              ("flags", L.SSM_SKIP, b"conv flags"), ("flags", L.SSM_COMPLEMENT, b"COMPLEMENT"),
+                              ("dtype", 5, b"dtype"), ("seqlen", 0, b"seqlen")]:
+        bad = L.SsmConvDesc(**{**good, field: value})
+        assert lib.ssm_conv_fwd(None, ctypes.byref(bad), p, p, p) == L.SSM_ERR_INVALID, field
+        assert msg in lib.ssm_last_error(), (field, lib.ssm_last_error())
+    assert lib.ssm_conv_fwd(None, ctypes.byref(d), None, p, p) == L.SSM_ERR_INVALID
+    assert lib.ssm_conv_bwd(None, ctypes.byref(d), p, p, p, p, p, None) == L.SSM_ERR_INVALID
+    assert b"workspace" in lib.ssm_last_error()

@@ -1,0 +1,112 @@
+"""GPU parity of the causal depthwise conv + activation (selectssm.py:167-185)
+against the fp64 oracle (rtol 1e-4 / atol 1e-5 for fp32 I/O; 2e-2 x max|ref|
+for bf16 I/O, the oracle run on the bf16-rounded inputs).  The flip maps are
+checked bitwise against explicit torch.flip of the input.
+"""
+import numpy as np
+import pytest
+
+from oracle import ssm_oracle as O
+
+from test_gpu_scan import _close, _cuda
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(B, L, D, K, seed):
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal((B, L, D)).astype(np.float32),
+            (rng.standard_normal((K, 1, D)) / np.sqrt(K)).astype(np.float32),
+            rng.standard_normal((B, L, D)).astype(np.float32))
+
+
+def _run(x, w, g, dtype=torch.float32, **kw):
+    from selectssm_amd import conv1d_act
+
+    xt = _cuda(x).to(dtype).requires_grad_(True)
+    wt = _cuda(w).requires_grad_(True)
+    u = conv1d_act(xt, wt, **kw)
+    u.backward(_cuda(g).to(dtype))
+    torch.cuda.synchronize()
+    return u, xt.grad, wt.grad
+
+
+@pytest.mark.parametrize("shape", [(2, 300, 70, 4), (1, 129, 64, 3), (3, 8, 5, 1), (2, 1000, 130, 8),
+                                   (1, 1, 3, 4), (2, 256, 256, 2)], ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("activation", ["silu", "relu", None])
+def test_conv_matches_oracle(shape, activation):
+    B, L, D, K = shape
+    print(f"conv shape={shape} activation={activation}", flush=True)
+    x, w, g = _inputs(B, L, D, K, seed=sum(shape))
+    u, dx, dw = _run(x, w, g, activation=activation)
+    w2 = w.reshape(K, D)
+    _close("u", u, O.conv_act_forward(x, w2, activation))
+    rdx, rdw = O.conv_act_backward(x, w2, g, activation)
+    _close("dx", dx, rdx)
+    _close("dw", dw.reshape(K, D), rdw, atol=1e-4)
+
+
+@pytest.mark.parametrize("rev,comp", [(True, False), (True, True)])
+def test_conv_flip_maps_match_oracle(rev, comp):
+    x, w, g = _inputs(2, 200, 96, 4, seed=3)
+    u, dx, dw = _run(x, w, g, reverse=rev, complement=comp)
+    w2 = w.reshape(4, 96)
+    _close("u", u, O.conv_act_forward(x, w2, "silu", rev, comp))
+    rdx, rdw = O.conv_act_backward(x, w2, g, "silu", rev, comp)
+    _close("dx", dx, rdx)
+    _close("dw", dw.reshape(4, 96), rdw, atol=1e-4)
+
+
+def test_conv_flip_maps_are_exact():
+    """reverse(+complement) == the unflipped conv of the explicitly flipped input, bitwise."""
+    from selectssm_amd import conv1d_act
+
+    x, w, _ = _inputs(2, 333, 100, 4, seed=4)
+    xt, wt = _cuda(x), _cuda(w)
+    assert torch.equal(conv1d_act(xt, wt, reverse=True), conv1d_act(torch.flip(xt, dims=(1,)), wt))
+    assert torch.equal(conv1d_act(xt, wt, reverse=True, complement=True),
+                       conv1d_act(torch.flip(xt, dims=(1, 2)), wt))
+    # complement without reverse is ignored, as in the reference
+    assert torch.equal(conv1d_act(xt, wt, complement=True), conv1d_act(xt, wt))
+
+
+def test_conv_bf16_matches_oracle():
+    x, w, g = _inputs(2, 256, 128, 4, seed=5)
+    xb = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    gb = torch.from_numpy(g).to(torch.bfloat16).float().numpy()
+    u, dx, dw = _run(xb, w, gb, dtype=torch.bfloat16)
+    w2 = w.reshape(4, 128)
+    ru = O.conv_act_forward(xb, w2)
+    rdx, rdw = O.conv_act_backward(xb, w2, gb)
+    at = lambda r: 2e-2 * max(1.0, float(np.abs(r).max()))
+    _close("u", u, ru, 2e-2, at(ru))
+    _close("dx", dx, rdx, 2e-2, at(rdx))
+    _close("dw", dw.reshape(4, 128), rdw, 2e-2, at(rdw))
+
+
+def test_conv_deterministic_and_partial_grads():
+    from selectssm_amd.conv import conv_bwd, conv_fwd
+
+    x, w, g = _inputs(2, 500, 200, 4, seed=6)
+    xt, wt, gt = _cuda(x), _cuda(w.reshape(4, 200)), _cuda(g)
+    dx1, dw1 = conv_bwd(xt, wt, gt)
+    dx2, dw2 = conv_bwd(xt, wt, gt)
+    assert torch.equal(dx1, dx2) and torch.equal(dw1, dw2)
+    dx3, none = conv_bwd(xt, wt, gt, need_dw=False)
+    assert none is None and torch.equal(dx3, dx1)
+    none, dw3 = conv_bwd(xt, wt, gt, need_dx=False)
+    assert none is None and torch.equal(dw3, dw1)
+    assert torch.equal(conv_fwd(xt, wt), conv_fwd(xt, wt))
+
+
+def test_conv_config1_width():
+    """Config-1 width and length (D=2048, L=8192) on two batch rows against the oracle."""
+    x, w, g = _inputs(2, 8192, 2048, 4, seed=7)
+    u, dx, dw = _run(x, w, g, reverse=True, complement=True)
+    w2 = w.reshape(4, 2048)
+    _close("u", u, O.conv_act_forward(x, w2, "silu", True, True))
+    rdx, rdw = O.conv_act_backward(x, w2, g, "silu", True, True)
+    _close("dx", dx, rdx)
+    _close("dw", dw.reshape(4, 2048), rdw, rtol=1e-4, atol=1e-3)

@@ -57,7 +57,8 @@ def _run(inp, flags=(), dtype=torch.float32):
     t["D"].requires_grad_(True)
     D = t["D"] if "skip" in flags else None
     z = t["z"] if "gate" in flags else None
-    y = selective_scan(t["u"], t["dt"], t["A"], t["B"], t["C"], D=D, z=z, reverse=reverse, complement=complement)
+    y = selective_scan(t["u"], t["dt"], t["A"], t["B"], t["C"], D=D, z=z, reverse=reverse, complement=complement,
+                       delta_softplus="softplus" in flags)
     y.backward(t["g"].to(dtype))
     torch.cuda.synchronize()
     grads = {k: (t[k].grad if t[k].grad is not None else None) for k in ("u", "dt", "A", "B", "C", "D", "z")}
@@ -66,7 +67,7 @@ def _run(inp, flags=(), dtype=torch.float32):
 
 def _oracle(inp, flags=()):
     kw = dict(Dskip=inp["D"] if "skip" in flags else None, z=inp["z"] if "gate" in flags else None,
-              reverse="reverse" in flags, complement="complement" in flags)
+              reverse="reverse" in flags, complement="complement" in flags, delta_softplus="softplus" in flags)
     y = O.ssm_block_forward(inp["u"], inp["dt"], inp["A"], inp["B"], inp["C"], **kw)
     du, ddt, dA, dB, dC, dD, dz = O.ssm_block_backward(inp["u"], inp["dt"], inp["A"], inp["B"], inp["C"],
                                                         inp["g"], **kw)
@@ -98,6 +99,33 @@ def test_scan_fp32_matches_oracle(shape):
 def test_epilogue_flags_match_oracle(flags):
     inp = make_inputs(2, 77, 96, 16, seed=2)
     _compare(inp, flags)
+
+
+def _pre_softplus(inp):
+    """Replace dt by the pre-activation of the same delta (softplus is fused in the scan)."""
+    inp = dict(inp)
+    inp["dt"] = np.log(np.expm1(inp["dt"].astype(np.float64))).astype(np.float32)
+    return inp
+
+
+@pytest.mark.parametrize("flags", [("softplus",), ("softplus", "reverse", "complement", "skip", "gate")],
+                         ids=lambda f: "+".join(f))
+def test_fused_delta_softplus_matches_oracle(flags):
+    inp = _pre_softplus(make_inputs(2, 77, 96, 16, seed=12))
+    _compare(inp, flags)
+
+
+def test_fused_delta_softplus_broadcast_and_split():
+    from test_gpu_segments import _run as run_seg
+
+    inp = _pre_softplus(make_inputs(2, 300, 40, 8, seed=13, delta_broadcast=True))
+    _compare(inp, ("softplus",))
+    inp = _pre_softplus(make_inputs(2, 300, 40, 8, seed=14))
+    y, g = run_seg(inp, ("softplus", "skip"), segments=4)
+    yr, gr = _oracle(inp, ("softplus", "skip"))
+    _close("y", y, yr)
+    for k in ("u", "dt", "A", "B", "C", "D"):
+        _close("d" + k, g[k], gr[k])
 
 
 def test_delta_broadcast_matches_oracle():

@@ -34,7 +34,7 @@ def _run(inp, flags=(), dtype=torch.float32, segments=0):
     t["D"].requires_grad_(True)
     y = selective_scan(t["u"], t["dt"], t["A"], t["B"], t["C"], D=t["D"] if "skip" in flags else None,
                        z=t["z"] if "gate" in flags else None, reverse="reverse" in flags,
-                       complement="complement" in flags, segments=segments)
+                       complement="complement" in flags, segments=segments, delta_softplus="softplus" in flags)
     y.backward(t["g"].to(dtype))
     torch.cuda.synchronize()
     return y, {k: t[k].grad for k in ("u", "dt", "A", "B", "C", "D", "z")}

@@ -249,13 +249,31 @@ def test_block_forward_reverse_skip_quirk_and_gate():
     assert O.flip_domain(u, True)[1, 0, 0] == u[1, -1, -1]
 
 
+def test_softplus_closed_forms():
+    x = np.linspace(-30, 30, 601)
+    # log(1 + e^x) where it is representable directly, x and e^x at the tails
+    mid = np.abs(x) < 15
+    np.testing.assert_allclose(O.softplus(x[mid]), np.log1p(np.exp(x[mid])), rtol=1e-14)
+    np.testing.assert_allclose(O.softplus(x[x > 25]), x[x > 25], rtol=1e-10)
+    np.testing.assert_allclose(O.softplus(x[x < -25]), np.exp(x[x < -25]), rtol=1e-10)
+    # softplus' = sigmoid, by central differences
+    h = 1e-6
+    np.testing.assert_allclose((O.softplus(x + h) - O.softplus(x - h)) / (2 * h), O.sigmoid(x), atol=1e-8)
+    # the synthetic delta is softplus(0.5 N(0,1) - 4): softplus(-4) = log(1 + e^-4)
+    assert abs(O.softplus(-4.0) - 0.01814992791780973) < 1e-15
+
+
 @pytest.mark.parametrize("flags", [dict(), dict(skip=1), dict(gate=1), dict(skip=1, gate=1, reverse=1),
-                                   dict(skip=1, gate=1, reverse=1, complement=1)])
+                                   dict(skip=1, gate=1, reverse=1, complement=1), dict(softplus=1),
+                                   dict(softplus=1, skip=1, gate=1, reverse=1)])
 def test_block_backward_finite_differences(flags):
     x = _rand((1, 9, 4, 2), 13)
     x["D"] = x["D"] * np.linspace(0.5, 1.5, 4)
+    if flags.get("softplus"):
+        x["dt"] = np.log(np.expm1(x["dt"]))  # the pre-activation of the same delta
     kw = dict(Dskip=x["D"] if flags.get("skip") else None, z=x["z"] if flags.get("gate") else None,
-              reverse=bool(flags.get("reverse")), complement=bool(flags.get("complement")))
+              reverse=bool(flags.get("reverse")), complement=bool(flags.get("complement")),
+              delta_softplus=bool(flags.get("softplus")))
     keys = ["u", "dt", "A", "B", "C"]
     grads = O.ssm_block_backward(x["u"], x["dt"], x["A"], x["B"], x["C"], x["g"], **kw)
     named = dict(zip(keys + ["D", "z"], grads))
@@ -334,3 +352,28 @@ def test_c_port_f64_matches_numpy_oracle(shape, ml, sp):
     ref = O.scan_backward(*args, x["g"])
     for a, r, name in zip(got, ref, ("du", "ddt", "dA", "dB", "dC")):
         np.testing.assert_allclose(a, r, rtol=1e-10, atol=1e-12, err_msg=name)
+
+
+@pytest.mark.parametrize("activation", ["silu", "relu", None])
+@pytest.mark.parametrize("rev,comp", [(False, False), (True, False), (True, True)])
+def test_conv_act_flip_composition_and_fd(activation, rev, comp):
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((2, 17, 6))
+    w = rng.standard_normal((3, 6))
+    u = O.conv_act_forward(x, w, activation, rev, comp)
+    # the flip is applied to x before the conv, by index: x_s[b,t,d] = x[b,L-1-t,(D-1-d)]
+    xs = x[:, ::-1, ::-1] if comp else (x[:, ::-1, :] if rev else x)
+    v = np.zeros_like(x)
+    for t in range(17):
+        for k in range(3):
+            if t - 2 + k >= 0:
+                v[:, t, :] += w[k] * xs[:, t - 2 + k, :]
+    ref = {"silu": v / (1 + np.exp(-v)), "relu": np.maximum(v, 0), None: v}[activation]
+    np.testing.assert_allclose(u, ref, rtol=1e-13, atol=1e-13)
+    g = rng.standard_normal(u.shape)
+    dx, dw = O.conv_act_backward(x, w, g, activation, rev, comp)
+    loss = lambda xx, ww: float(np.sum(O.conv_act_forward(xx, ww, activation, rev, comp) * g))
+    vx, vw = rng.standard_normal(x.shape), rng.standard_normal(w.shape)
+    eps = 1e-6
+    fd = (loss(x + eps * vx, w + eps * vw) - loss(x - eps * vx, w - eps * vw)) / (2 * eps)
+    np.testing.assert_allclose(fd, np.sum(dx * vx) + np.sum(dw * vw), rtol=1e-6)
