@@ -29,6 +29,13 @@ Pinning (what checks each function, in ``tests/test_oracle.py``):
   causal_conv1d(_bwd)     numpy.convolve per channel; finite differences
   conv_act_forward/_bwd   explicit np.flip composition, relu/silu closed forms;
                           finite differences
+  selective_ssm_forward   the pinned pieces above composed as selectssm.py:146-238;
+                          the reverse map and skip quirk checked as an identity
+                          between the reverse module and the forward module on
+                          the flipped input; reduces to scan_forward + skip for
+                          a unit 1-tap conv, no activation and identity dt
+  bidirectional_mamba_forward  composition of selectssm.py:282-364; split /
+                          tie / concat checked against explicit slicing
   ssm_block_forward/_bwd  explicit np.flip composition; finite differences
 """
 from __future__ import annotations
@@ -294,13 +301,24 @@ def conv1d_silu_backward(x, w, du):
     return causal_conv1d_backward(x, w, dv)
 
 
+def gelu_tanh(x):
+    """0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))): flax.linen.gelu's default
+    (approximate=True).  That default lives in Flax, not in the reference:
+    parity unpinned beyond this closed form."""
+    x = np.asarray(x, np.float64)
+    return 0.5 * x * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (x + 0.044715 * x ** 3)))
+
+
 def activate(x, activation):
-    """SelectiveSSM's activation after the conv (selectssm.py:176-185): silu, relu or none."""
+    """SelectiveSSM's activation after the conv (selectssm.py:176-185) and
+    BidirectionalMamba's gate activation (298-305): silu, relu, gelu or none."""
     x = np.asarray(x, np.float64)
     if activation == "silu":
         return silu(x)
     if activation == "relu":
         return np.maximum(x, 0.0)
+    if activation == "gelu":
+        return gelu_tanh(x)
     if activation is None or activation == "none":
         return x
     raise ValueError(activation)
@@ -331,6 +349,96 @@ def conv_act_backward(x, w, du, activation="silu", reverse=False, complement=Fal
     dv = np.asarray(du, np.float64) * activate_grad(causal_conv1d(xs, w), activation)
     dxs, dw = causal_conv1d_backward(xs, w, dv)
     return (flip_domain(dxs, complement) if reverse else dxs), dw
+
+
+# --------------------------------------------------------------------------
+# Modules (selectssm.py:112-364) with explicit Flax-named parameter dicts
+# --------------------------------------------------------------------------
+
+def dense(x, p):
+    """flax.linen.Dense: x @ kernel + bias, kernel (in, out)."""
+    y = np.asarray(x, np.float64) @ np.asarray(p["kernel"], np.float64)
+    return y + np.asarray(p["bias"], np.float64) if "bias" in p else y
+
+
+def selective_ssm_forward(p, x, reverse=False, complement=False, hidden_features=16, dt_rank="auto",
+                          dt_proj=True, activation="silu", gate=None, gate_activation="silu", **_unused):
+    """SelectiveSSM.__call__ (selectssm.py:146-238) in fp64; ``gate`` applies
+    BidirectionalMamba's ``y * activate(z)`` (selectssm.py:335-336).  The chunk /
+    recursion arguments do not change y and are not taken."""
+    x = np.asarray(x, np.float64)
+    D = x.shape[-1]
+    N = hidden_features
+    R = math.ceil(D / 16) if dt_rank == "auto" else dt_rank                       # 158-161
+    xs = flip_domain(x, complement) if reverse else x                             # 167-168
+    w = np.asarray(p["shift_conv"]["kernel"], np.float64)
+    u = activate(causal_conv1d(xs, w.reshape(w.shape[0], D)), activation)          # 170-187
+    A = -np.exp(np.asarray(p["A_log"], np.float64))                               # 190
+    BC = dense(u, p["BC"])                                                         # 191
+    Bc, Cc = BC[..., :N], BC[..., N:]
+    dt = dense(u, p["dt"])                                                         # 195-197
+    if dt_proj:
+        dt = dense(dt, p["dt_proj"])                                               # 203-204
+    elif R > 1:
+        dt = np.repeat(dt, D // R, axis=-1)                                        # 206-209
+    dt = softplus(dt)                                                              # 210
+    y = scan_forward(u, dt, A, Bc, Cc)                                             # 222-228
+    if reverse:
+        y = flip_domain(y, complement)                                             # 230-231
+    y = y + u * np.asarray(p["D"], np.float64)                                     # 238
+    if gate is not None:
+        y = y * activate(gate, gate_activation)
+    return y
+
+
+def rms_norm(x, scale, eps=1e-6):
+    """flax.linen.RMSNorm (epsilon default 1e-6: a Flax default, parity unpinned)."""
+    x = np.asarray(x, np.float64)
+    return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps) * np.asarray(scale, np.float64)
+
+
+def layer_norm(x, scale, bias, eps=1e-6):
+    """flax.linen.LayerNorm (epsilon default 1e-6: a Flax default, parity unpinned)."""
+    x = np.asarray(x, np.float64)
+    m = x.mean(-1, keepdims=True)
+    v = ((x - m) ** 2).mean(-1, keepdims=True)
+    return (x - m) / np.sqrt(v + eps) * np.asarray(scale, np.float64) + np.asarray(bias, np.float64)
+
+
+def bidirectional_mamba_forward(p, x, hidden_features, expansion_factor, dt_rank="auto", complement=False,
+                                tie_in_proj=False, tie_gate=False, concatenate_fwd_rev=True, activation="silu",
+                                norm_type="rms", mlp_layer=False, ssm_args=None):
+    """BidirectionalMamba.__call__ (selectssm.py:282-364) in fp64, inference mode
+    (no dropout, batch statistics not updated)."""
+    ssm_args = dict(ssm_args or {})
+    x = np.asarray(x, np.float64)
+    D = x.shape[-1]
+    R = math.ceil(D / 16) if dt_rank == "auto" else dt_rank                       # 286-289
+    skip = x
+    if norm_type == "rms":
+        x = rms_norm(x, p["RMSNorm_0"]["scale"])
+    elif norm_type == "layer":
+        x = layer_norm(x, p["LayerNorm_0"]["scale"], p["LayerNorm_0"]["bias"])
+    elif norm_type is not None:
+        raise ValueError(norm_type)
+    ED = math.ceil(expansion_factor * D)                                           # 315
+    n_in = 1 if tie_in_proj else 2
+    n_gate = 1 if tie_gate else 2
+    h = dense(x, p["in_proj"])
+    xf, _xr, zf, _zr = np.split(h, [ED, n_in * ED, (n_in + 1) * ED], axis=-1)      # 319
+    xr = xf if tie_in_proj else _xr                                                # 320
+    zr = zf if tie_gate else _zr                                                   # 321
+    yf = selective_ssm_forward(p["ssm_fwd"], xf, reverse=False, hidden_features=hidden_features, dt_rank=R,
+                               gate=zf, gate_activation=activation, **ssm_args)    # 325
+    yr = selective_ssm_forward(p["ssm_rev"], xr, reverse=True, complement=complement,
+                               hidden_features=hidden_features, dt_rank=R, gate=zr, gate_activation=activation,
+                               **ssm_args)                                         # 326
+    x = np.concatenate([yf, yr], axis=-1) if concatenate_fwd_rev else yf + yr      # 335-338
+    x = skip + dense(x, p["out_proj"])                                             # 345-352
+    if mlp_layer:
+        skip = x
+        x = skip + dense(activate(dense(x, p["mlp"]), activation), p["mlp_proj"])  # 354-362
+    return x
 
 
 # --------------------------------------------------------------------------

@@ -7,6 +7,7 @@ hand-written HIP kernels exported through the C ABI in ``include/selectssm.h``.
 There is no CPU fallback.
 """
 from .conv import conv1d_act
+from .modules import BidirectionalMamba, SelectiveSSM
 from .scan import (
     SelectiveScanFn,
     largest_factor_up_to,
@@ -18,6 +19,8 @@ from .scan import (
 )
 
 __all__ = [
+    "BidirectionalMamba",
+    "SelectiveSSM",
     "SelectiveScanFn",
     "conv1d_act",
     "largest_factor_up_to",

@@ -1,0 +1,432 @@
+"""``SelectiveSSM`` and ``BidirectionalMamba`` as torch modules over the HIP kernels.
+
+Same constructor fields, defaults, parameter tree and call signature as the
+reference's Flax modules (selectssm.py:112-238 and 240-364); a Flax parameter
+tree loads 1:1 with :meth:`load_flax_params` (Flax ``a/b`` is torch ``a.b``;
+Dense kernels keep Flax's (in, out) layout).  Like Flax modules, the parameters
+take their shapes from the first input unless ``features`` is given.
+
+The hot path is fused:
+  * flip + ``shift_conv`` + activation  -> one ``ssm_conv_fwd`` launch
+  * softplus(dt), the scan, the un-flip, the D skip (with the reference's
+    flipped-domain ``u``), and in BidirectionalMamba the silu gate
+                                        -> one ``ssm_fwd`` launch
+  * the Dense projections (BC, dt, dt_proj, in_proj, out_proj) run on hipBLASLt
+    through torch.
+Every strategy flag (chunked / ``recursive_scan`` / ``custom_vjp_scan``) runs the
+same kernels after the reference's own argument checks (the strategies agree
+up to fp32 rounding); the backward is the custom VJP's adjoint.
+
+Activations are computed in the input's dtype (float32, or bfloat16 with fp32
+scan state and accumulation); parameters are float32.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Union
+
+import torch
+import torch.nn.functional as F
+
+from .conv import conv1d_act
+from .scan import _check_recursion, resolve_chunking, selective_scan
+
+_FUSED_CONV_ACTS = ("silu", "relu", None)
+
+
+def _activation_fn(name):
+    if name == "gelu":
+        return lambda t: F.gelu(t, approximate="tanh")  # flax.linen.gelu default: tanh approximation
+    if name == "silu":
+        return F.silu
+    if name == "relu":
+        return F.relu
+    raise Exception(f"Unknown activation: {name}")
+
+
+def lecun_normal_(t: torch.Tensor, fan_in: int, generator=None) -> torch.Tensor:
+    """Truncated normal in [-2, 2] std units with variance 1/fan_in (lecun_normal)."""
+    std = math.sqrt(1.0 / fan_in) / 0.87962566103423978  # std of a unit normal truncated to [-2, 2]
+    with torch.no_grad():
+        t.normal_(0.0, 1.0, generator=generator)
+        # redraw outside [-2, 2] until none remain
+        for _ in range(100):
+            bad = t.abs() > 2
+            if not bad.any():
+                break
+            t[bad] = torch.randn(int(bad.sum()), device=t.device, dtype=t.dtype, generator=generator)
+        t.clamp_(-2, 2).mul_(std)
+    return t
+
+
+def inverse_softplus(x):
+    """x + log(1 - e^-x) (selectssm.py:18-19)."""
+    return x + torch.log(-torch.expm1(-x))
+
+
+class Dense(torch.nn.Module):
+    """flax.linen.Dense: y = x @ kernel + bias, kernel (in, out)."""
+
+    def __init__(self, in_features, out_features, use_bias=True, device=None, generator=None, bias_init=None):
+        super().__init__()
+        self.kernel = torch.nn.Parameter(lecun_normal_(torch.empty(in_features, out_features, device=device),
+                                                       in_features, generator))
+        if use_bias:
+            b = torch.zeros(out_features, device=device) if bias_init is None else bias_init
+            self.bias = torch.nn.Parameter(b)
+        else:
+            self.register_parameter("bias", None)
+
+    def forward(self, x):
+        w = self.kernel.to(x.dtype)
+        x2 = x.reshape(-1, x.shape[-1])
+        y = x2 @ w if self.bias is None else torch.addmm(self.bias.to(x.dtype), x2, w)
+        return y.reshape(*x.shape[:-1], w.shape[1])
+
+
+class _ShiftConv(torch.nn.Module):
+    def __init__(self, K, D, device=None, generator=None):
+        super().__init__()
+        # Flax Conv kernel (K, in/groups = 1, D); fan_in = K * 1
+        self.kernel = torch.nn.Parameter(lecun_normal_(torch.empty(K, 1, D, device=device), K, generator))
+
+
+class _FlaxModule(torch.nn.Module):
+    """Lazy build on first call + Flax parameter-tree import / export."""
+
+    def load_flax_params(self, params: dict) -> None:
+        """Copy a Flax parameter tree (nested dict of arrays, no 'params' root) into this module."""
+        flat = {}
+
+        def walk(prefix, tree):
+            for k, v in tree.items():
+                if isinstance(v, dict):
+                    walk(prefix + k + ".", v)
+                else:
+                    flat[prefix + k] = v
+
+        walk("", params)
+        own = dict(self.named_parameters())
+        if set(flat) != set(own):
+            raise ValueError(f"parameter trees differ: missing {sorted(set(own) - set(flat))}, "
+                             f"unexpected {sorted(set(flat) - set(own))}")
+        with torch.no_grad():
+            for k, v in flat.items():
+                t = torch.as_tensor(v)
+                if tuple(t.shape) != tuple(own[k].shape):
+                    raise ValueError(f"{k}: shape {tuple(t.shape)} != {tuple(own[k].shape)}")
+                own[k].copy_(t)
+
+    def flax_params(self) -> dict:
+        """This module's parameters as a Flax-style nested dict of CPU tensors."""
+        tree = {}
+        for name, p in self.named_parameters():
+            node = tree
+            *path, leaf = name.split(".")
+            for part in path:
+                node = node.setdefault(part, {})
+            node[leaf] = p.detach().cpu()
+        return tree
+
+
+class SelectiveSSM(_FlaxModule):
+    """A variation on MAMBA (selectssm.py:112-238), on MI355X kernels."""
+
+    def __init__(self, reverse: bool = False, complement: bool = False, hidden_features: int = 16,
+                 chunk_size: Optional[int] = None, n_channel_groups: Optional[int] = None,
+                 dt_rank: Union[int, str] = "auto", dt_proj: bool = True, dt_min: float = 0.001,
+                 dt_max: float = 0.1, regularize: bool = True, shift_l2_scale: float = 1e-7,
+                 ssm_l2_scale: float = 1e-6, shift_conv_size: int = 3, activation: str = "silu",
+                 diagnostics: Optional[dict] = None, recursive_scan: bool = False, min_recursion_length: int = 2,
+                 recursive_split: int = 2, custom_vjp_scan: bool = False, features: Optional[int] = None,
+                 device=None, generator: Optional[torch.Generator] = None):
+        super().__init__()
+        self.reverse = reverse
+        self.complement = complement
+        self.hidden_features = hidden_features
+        self.chunk_size = chunk_size
+        self.n_channel_groups = n_channel_groups
+        self.dt_rank = dt_rank
+        self.dt_proj_enabled = dt_proj
+        self.dt_min = dt_min
+        self.dt_max = dt_max
+        self.regularize = regularize
+        self.shift_l2_scale = shift_l2_scale
+        self.ssm_l2_scale = ssm_l2_scale
+        self.shift_conv_size = shift_conv_size
+        self.activation = activation
+        self.diagnostics = dict(diagnostics or {})
+        self.recursive_scan = recursive_scan
+        self.min_recursion_length = min_recursion_length
+        self.recursive_split = recursive_split
+        self.custom_vjp_scan = custom_vjp_scan
+        self.generator = generator
+        self.sown = {}
+        self.features = None
+        if features is not None:
+            self._build(features, device)
+
+    def _build(self, D, device):
+        N = self.hidden_features
+        R = math.ceil(D / 16) if self.dt_rank == "auto" else int(self.dt_rank)
+        g = self.generator
+        self.features, self.rank = D, R
+        self.shift_conv = _ShiftConv(self.shift_conv_size, D, device, g)
+        # A = -exp(A_log), A_log initialised to log(1..N) per channel (selectssm.py:190)
+        self.A_log = torch.nn.Parameter(torch.log(torch.arange(1, N + 1, dtype=torch.float32, device=device))
+                                        .repeat(D, 1))
+        self.BC = Dense(D, 2 * N, device=device, generator=g)
+        self.D = torch.nn.Parameter(torch.ones(D, device=device))
+        lo, hi = self.dt_min, self.dt_max
+
+        def dt_bias(n):
+            r = torch.rand(n, device=device, generator=g) * (hi - lo) + lo
+            return inverse_softplus(r)
+
+        self.dt = Dense(D, R, device=device, generator=g, bias_init=None if self.dt_proj_enabled else dt_bias(R))
+        if self.dt_proj_enabled:
+            self.dt_proj = Dense(R, D, device=device, generator=g, bias_init=dt_bias(D))
+
+    def _sow(self, col, name, value):
+        self.sown.setdefault(col, {})[name] = value
+
+    def forward(self, x: torch.Tensor, train: bool = False, gate: Optional[torch.Tensor] = None,
+                gate_activation: str = "silu") -> torch.Tensor:
+        """y (B, L, D) for x (B, L, D).  ``gate`` (BidirectionalMamba's z) multiplies the
+        output by gate_activation(z) (selectssm.py:335-336), fused into the scan for silu."""
+        if self.features is None:
+            self._build(x.shape[-1], x.device)
+        B, L, D = x.shape
+        if D != self.features:
+            raise ValueError(f"x has {D} features, the module was built for {self.features}")
+        N = self.hidden_features
+        self.sown = {}
+        diag = self.diagnostics
+        if diag and "ssm_input_norm" in diag:
+            self._sow("diagnostics", "ssm_input_mean", x.mean())
+            self._sow("diagnostics", "ssm_input_sd", x.std(unbiased=False))
+
+        # flip + shift_conv + activation (selectssm.py:167-185), one kernel; the
+        # activation runs separately for gelu and when the raw conv output is sown
+        if self.activation not in _FUSED_CONV_ACTS and self.activation != "gelu":
+            raise Exception(f"Unknown activation: {self.activation}")
+        coeffs = bool(diag) and "ssm_coeffs" in diag
+        fused = self.activation in _FUSED_CONV_ACTS and not coeffs
+        u = conv1d_act(x, self.shift_conv.kernel, self.reverse, self.complement,
+                       self.activation if fused else None)
+        if coeffs:
+            self._sow("diagnostics", "conv_mean", u.mean())
+            self._sow("diagnostics", "conv_sd", u.std(unbiased=False))
+        if not fused and self.activation is not None:
+            u = _activation_fn(self.activation)(u)
+
+        A = -torch.exp(self.A_log)
+        BC = self.BC(u)
+        Bc, Cc = BC[..., :N], BC[..., N:]
+        dt = self.dt(u)
+        if self.dt_proj_enabled:
+            dt = self.dt_proj(dt)
+        elif self.rank > 1:
+            if D % self.rank != 0:
+                raise ValueError(f"dt_rank={self.rank} must divide D={D}")
+            dt = torch.repeat_interleave(dt, D // self.rank, dim=-1)
+        if coeffs:
+            self._sow("diagnostics", "dt_lowrank_mean", self.dt(u).mean())
+            dsp = F.softplus(dt)
+            for k, v in (("activated_conv_mean", u.mean()), ("activated_conv_sd", u.std(unbiased=False)),
+                         ("dt_mean", dsp.mean()), ("dt_sd", dsp.std(unbiased=False)), ("A_mean", A.mean()),
+                         ("A_sd", A.std(unbiased=False)), ("B_sd", Bc.std(unbiased=False)),
+                         ("C_sd", Cc.std(unbiased=False))):
+                self._sow("diagnostics", k, v)
+
+        # the reference's strategy dispatch (selectssm.py:223-228) and its argument checks
+        if self.custom_vjp_scan or self.recursive_scan:
+            _check_recursion(self.min_recursion_length, self.recursive_split)
+        else:
+            resolve_chunking(L, D, self.chunk_size, self.n_channel_groups)
+
+        fuse_gate = gate is not None and gate_activation == "silu"
+        y = selective_scan(u, dt, A, Bc, Cc, D=self.D, z=gate if fuse_gate else None, reverse=self.reverse,
+                           complement=self.complement, delta_softplus=True)
+        if gate is not None and not fuse_gate:
+            y = y * _activation_fn(gate_activation)(gate)
+
+        if self.regularize:
+            kernels = [self.BC.kernel, self.dt.kernel] + ([self.dt_proj.kernel] if self.dt_proj_enabled else [])
+            reg = (self.shift_l2_scale * torch.sum(self.shift_conv.kernel ** 2)
+                   + self.ssm_l2_scale * sum(torch.sum(k ** 2) for k in kernels))
+            self._sow("losses", "ssm_regularizer", reg)
+        if diag and "ssm_output_norm" in diag:
+            self._sow("diagnostics", "ssm_output_mean", y.mean())
+            self._sow("diagnostics", "ssm_output_sd", y.std(unbiased=False))
+        return y
+
+
+class RMSNorm(torch.nn.Module):
+    """flax.linen.RMSNorm (epsilon 1e-6, learned scale), computed in float32."""
+
+    def __init__(self, D, eps=1e-6, device=None):
+        super().__init__()
+        self.eps = eps
+        self.scale = torch.nn.Parameter(torch.ones(D, device=device))
+
+    def forward(self, x):
+        xf = x.float()
+        y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps) * self.scale
+        return y.to(x.dtype)
+
+
+class LayerNorm(torch.nn.Module):
+    """flax.linen.LayerNorm (epsilon 1e-6, learned scale and bias), computed in float32."""
+
+    def __init__(self, D, eps=1e-6, device=None):
+        super().__init__()
+        self.eps = eps
+        self.scale = torch.nn.Parameter(torch.ones(D, device=device))
+        self.bias = torch.nn.Parameter(torch.zeros(D, device=device))
+
+    def forward(self, x):
+        return F.layer_norm(x.float(), (x.shape[-1],), self.scale, self.bias, self.eps).to(x.dtype)
+
+
+class GroupNorm(torch.nn.Module):
+    """flax.linen.GroupNorm (32 groups over the feature axis, epsilon 1e-6)."""
+
+    def __init__(self, D, groups=32, eps=1e-6, device=None):
+        super().__init__()
+        if D % groups != 0:
+            raise ValueError(f"GroupNorm: {groups} groups must divide {D} features")
+        self.groups, self.eps = groups, eps
+        self.scale = torch.nn.Parameter(torch.ones(D, device=device))
+        self.bias = torch.nn.Parameter(torch.zeros(D, device=device))
+
+    def forward(self, x):
+        B, L, D = x.shape
+        xf = x.float().reshape(B, L, self.groups, D // self.groups)
+        # statistics over every non-batch axis within a group (time and the group's features)
+        mean = xf.mean(dim=(1, 3), keepdim=True)
+        var = xf.var(dim=(1, 3), keepdim=True, unbiased=False)
+        y = ((xf - mean) * torch.rsqrt(var + self.eps)).reshape(B, L, D) * self.scale + self.bias
+        return y.to(x.dtype)
+
+
+class BatchNorm(torch.nn.Module):
+    """flax.linen.BatchNorm over (batch, time), momentum as Flax (running = m*running + (1-m)*batch)."""
+
+    def __init__(self, D, momentum=0.9, eps=1e-5, device=None):
+        super().__init__()
+        self.momentum, self.eps = momentum, eps
+        self.scale = torch.nn.Parameter(torch.ones(D, device=device))
+        self.bias = torch.nn.Parameter(torch.zeros(D, device=device))
+        self.register_buffer("mean", torch.zeros(D, device=device))
+        self.register_buffer("var", torch.ones(D, device=device))
+
+    def forward(self, x, train=False):
+        xf = x.float()
+        if train:
+            mean = xf.mean(dim=(0, 1))
+            var = xf.var(dim=(0, 1), unbiased=False)
+            with torch.no_grad():
+                self.mean.mul_(self.momentum).add_((1 - self.momentum) * mean)
+                self.var.mul_(self.momentum).add_((1 - self.momentum) * var)
+        else:
+            mean, var = self.mean, self.var
+        return ((xf - mean) * torch.rsqrt(var + self.eps) * self.scale + self.bias).to(x.dtype)
+
+
+class BidirectionalMamba(_FlaxModule):
+    """Bidirectional Mamba block (selectssm.py:240-364), on MI355X kernels."""
+
+    def __init__(self, hidden_features: int, expansion_factor: float, dt_rank: Union[int, str] = "auto",
+                 complement: bool = False, tie_in_proj: bool = False, tie_gate: bool = False,
+                 concatenate_fwd_rev: bool = True, activation: str = "silu", norm_type: str = "rms",
+                 bn_momentum: float = 0.9, mlp_layer: bool = False, dense_expansion: int = 2,
+                 mlp_dropout_rate: float = 0.1, ssm_args: Optional[dict] = None, diagnostics: Optional[dict] = None,
+                 features: Optional[int] = None, device=None, generator: Optional[torch.Generator] = None):
+        super().__init__()
+        self.hidden_features = hidden_features
+        self.expansion_factor = expansion_factor
+        self.dt_rank = dt_rank
+        self.complement = complement
+        self.tie_in_proj = tie_in_proj
+        self.tie_gate = tie_gate
+        self.concatenate_fwd_rev = concatenate_fwd_rev
+        self.activation = activation
+        self.norm_type = norm_type
+        self.bn_momentum = bn_momentum
+        self.mlp_layer = mlp_layer
+        self.dense_expansion = dense_expansion
+        self.mlp_dropout_rate = mlp_dropout_rate
+        self.ssm_args = dict(ssm_args or {})
+        self.diagnostics = dict(diagnostics or {})
+        self.generator = generator
+        self.sown = {}
+        self.features = None
+        _activation_fn(activation)  # unknown names raise at construction, as at the reference's first call
+        if features is not None:
+            self._build(features, device)
+
+    def _build(self, D, device):
+        g = self.generator
+        self.features = D
+        R = math.ceil(D / 16) if self.dt_rank == "auto" else self.dt_rank
+        if self.norm_type == "batch":
+            self.BatchNorm_0 = BatchNorm(D, self.bn_momentum, device=device)
+        elif self.norm_type == "layer":
+            self.LayerNorm_0 = LayerNorm(D, device=device)
+        elif self.norm_type == "group":
+            self.GroupNorm_0 = GroupNorm(D, device=device)
+        elif self.norm_type == "rms":
+            self.RMSNorm_0 = RMSNorm(D, device=device)
+        ED = math.ceil(self.expansion_factor * D)
+        self.ED = ED
+        n_in = 1 if self.tie_in_proj else 2
+        n_gate = 1 if self.tie_gate else 2
+        self.in_proj = Dense(D, (n_in + n_gate) * ED, device=device, generator=g)
+        self.ssm_fwd = SelectiveSSM(hidden_features=self.hidden_features, reverse=False, dt_rank=R,
+                                    diagnostics=self.diagnostics, **self.ssm_args, features=ED, device=device,
+                                    generator=g)
+        self.ssm_rev = SelectiveSSM(hidden_features=self.hidden_features, reverse=True, complement=self.complement,
+                                    dt_rank=R, diagnostics=self.diagnostics, **self.ssm_args, features=ED,
+                                    device=device, generator=g)
+        self.out_proj = Dense(2 * ED if self.concatenate_fwd_rev else ED, D, device=device, generator=g)
+        if self.mlp_layer:
+            self.mlp = Dense(D, self.dense_expansion * D, device=device, generator=g)
+            self.mlp_proj = Dense(self.dense_expansion * D, D, device=device, generator=g)
+
+    def forward(self, x: torch.Tensor, train: bool = False) -> torch.Tensor:
+        if self.features is None:
+            self._build(x.shape[-1], x.device)
+        activate = _activation_fn(self.activation)
+        skip = x
+        if self.norm_type == "batch":
+            x = self.BatchNorm_0(x, train)
+        elif self.norm_type == "layer":
+            x = self.LayerNorm_0(x)
+        elif self.norm_type == "group":
+            x = self.GroupNorm_0(x)
+        elif self.norm_type == "rms":
+            x = self.RMSNorm_0(x)
+        ED = self.ED
+        n_in = 1 if self.tie_in_proj else 2
+        h = self.in_proj(x)
+        # jnp.split at [ED, n_in*ED, (n_in+1)*ED] (selectssm.py:319-321)
+        xf, _xr = h[..., :ED], h[..., ED:n_in * ED]
+        zf, _zr = h[..., n_in * ED:(n_in + 1) * ED], h[..., (n_in + 1) * ED:]
+        xr = xf if self.tie_in_proj else _xr
+        zr = zf if self.tie_gate else _zr
+        # the gate of selectssm.py:335-336 is applied inside each SSM's scan epilogue
+        yf = self.ssm_fwd(xf, train, gate=zf, gate_activation=self.activation)
+        yr = self.ssm_rev(xr, train, gate=zr, gate_activation=self.activation)
+        x = torch.cat([yf, yr], dim=-1) if self.concatenate_fwd_rev else yf + yr
+        x = self.out_proj(x)
+        x = skip + x
+        if self.mlp_layer:
+            skip = x
+            x = self.mlp(x)
+            x = F.dropout(x, self.mlp_dropout_rate, training=train)
+            x = activate(x)
+            x = self.mlp_proj(x)
+            x = F.dropout(x, self.mlp_dropout_rate, training=train)
+            x = skip + x
+        return x

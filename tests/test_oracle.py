@@ -377,3 +377,47 @@ def test_conv_act_flip_composition_and_fd(activation, rev, comp):
     eps = 1e-6
     fd = (loss(x + eps * vx, w + eps * vw) - loss(x - eps * vx, w - eps * vw)) / (2 * eps)
     np.testing.assert_allclose(fd, np.sum(dx * vx) + np.sum(dw * vw), rtol=1e-6)
+
+
+def _ssm_params(rng, D, N=4, K=3, R=None, dt_proj=True):
+    R = R or -(-D // 16)
+    p = {"shift_conv": {"kernel": rng.standard_normal((K, 1, D)) / np.sqrt(K)},
+         "A_log": np.log(rng.uniform(1, 16, (D, N))),
+         "BC": {"kernel": rng.standard_normal((D, 2 * N)) / np.sqrt(D), "bias": rng.standard_normal(2 * N) * 0.1},
+         "D": rng.uniform(0.5, 1.5, D),
+         "dt": {"kernel": rng.standard_normal((D, R)) / np.sqrt(D), "bias": rng.standard_normal(R) * 0.1 - 4}}
+    if dt_proj:
+        p["dt_proj"] = {"kernel": rng.standard_normal((R, D)) / np.sqrt(R), "bias": rng.standard_normal(D) * 0.1 - 4}
+    return p
+
+
+@pytest.mark.parametrize("complement", [False, True])
+def test_selective_ssm_reverse_is_forward_on_flipped_input_plus_skip_quirk(complement):
+    """SelectiveSSM(reverse) flips x, runs the forward module's body, un-flips the scan
+    output and adds u*D with u left in the flipped domain (selectssm.py:167-168, 230-238):
+    rev(x) = flip(fwd(flip x) - u D) + u D, u = act(conv(flip x))."""
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((2, 12, 5))
+    p = _ssm_params(rng, 5)
+    xs = O.flip_domain(x, complement)
+    u = O.silu(O.causal_conv1d(xs, p["shift_conv"]["kernel"].reshape(3, 5)))
+    rev = O.selective_ssm_forward(p, x, reverse=True, complement=complement, hidden_features=4)
+    fwd = O.selective_ssm_forward(p, xs, hidden_features=4)
+    np.testing.assert_allclose(rev, O.flip_domain(fwd - u * p["D"], complement) + u * p["D"], rtol=1e-12,
+                               atol=1e-12)
+    # the quirk is visible: un-flipping the skip term too would give another answer
+    assert not np.allclose(rev, O.flip_domain(fwd, complement))
+
+
+def test_selective_ssm_reduces_to_scan_plus_skip():
+    """1-tap unit conv, no activation, dt_rank=1 without dt_proj (delta broadcast):
+    y = scan(x, softplus(dt), A, B, C) + x D with dt = x @ dt.kernel + dt.bias."""
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((2, 10, 6))
+    p = _ssm_params(rng, 6, K=1, R=1, dt_proj=False)
+    p["shift_conv"]["kernel"] = np.ones((1, 1, 6))
+    y = O.selective_ssm_forward(p, x, hidden_features=4, dt_rank=1, dt_proj=False, activation=None)
+    BC = x @ p["BC"]["kernel"] + p["BC"]["bias"]
+    dt = O.softplus(x @ p["dt"]["kernel"] + p["dt"]["bias"])
+    ref = O.scan_forward(x, dt, -np.exp(p["A_log"]), BC[..., :4], BC[..., 4:]) + x * p["D"]
+    np.testing.assert_allclose(y, ref, rtol=1e-12)
