@@ -51,7 +51,13 @@ constexpr int kCh = 32;   // channels per workgroup (lane & 31)
 constexpr int kSPW = 4;   // states per wave: 2 per lane, the two lane halves differ
 constexpr int kTT = 32;   // forward time tile
 constexpr int kCK = 16;   // checkpoint interval = backward block length
-constexpr int kRB = 4;    // backward steps per batched dB / dC reduction (4 steps x 2 states)
+#ifndef SSM_LDS_DB
+#define SSM_LDS_DB 1
+#endif
+#ifndef SSM_LDS_DC
+#define SSM_LDS_DC 0
+#endif
+constexpr int kRS = 36;   // padded row (floats) of the dB / dC transpose tile: 16-lane float4 reads hit distinct banks
 
 // --------------------------------------------------------------- forward
 
@@ -83,7 +89,9 @@ struct FwdArgs {
 //     its end from a zero start, and its sum of delta, so that
 //     h_end = exp(A * sum delta) * h_start + H (the combine of
 //     selectssm.py:81-85 applied to a whole segment).
-template <int NG, bool EPI, bool AGG, typename T>
+// SP: delta arrives before softplus (SSM_DELTA_SOFTPLUS); a separate build,
+// because carrying the unused softplus code in the time loop slows it down.
+template <int NG, bool EPI, bool AGG, bool SP, typename T>
 __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kernel(FwdArgs<T> p) {
   static_assert(!(EPI && AGG), "the aggregate pass has no epilogue");
   constexpr int NS = NG * kSPW;         // padded state count
@@ -115,7 +123,6 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kerne
   const bool skip = EPI && (p.flags & SSM_SKIP);
   const bool gate = EPI && (p.flags & SSM_GATE);
   const bool stage_eu = skip && rev;  // u at the output position is another element
-  const bool dsp = p.flags & SSM_DELTA_SOFTPLUS;
   // staging / output mapping: thread -> column scol, rows srow0 + k * RSTEP
   const int scol = tid & (kCh - 1);
   const int srow0 = tid / kCh;
@@ -212,8 +219,8 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kerne
     for (int k = 0; k < RPT; ++k) {
       const int i = srow0 + k * RSTEP;
       const bool in = svalid && t0 + i < L;
+      s_dt[buf][i][scol] = in ? (SP ? softplus(r_dt[k]) : r_dt[k]) : 0.0f;
       s_u[buf][i][scol] = in ? r_u[k] : 0.0f;
-      s_dt[buf][i][scol] = in ? (dsp ? softplus(r_dt[k]) : r_dt[k]) : 0.0f;
       if (stage_eu) s_eu[buf][i][scol] = in ? r_eu[k] : 0.0f;
       if (gate) s_ez[buf][i][scol] = in ? r_ez[k] : 0.0f;
     }
@@ -361,6 +368,13 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
   constexpr int RSTEP = NT / kCh;
   constexpr int BCE = kCK * NS / NT;
   static_assert(BCE * NT == kCK * NS && RPT * NT == kCK * kCh, "staging must tile exactly");
+  // dB and dC sums over the 32 channels of a wave half: through an LDS
+  // transpose tile (LDS_DB / LDS_DC) or in registers with cross-lane moves
+  constexpr bool kDbLds = SSM_LDS_DB != 0;
+  constexpr bool kDcLds = SSM_LDS_DC != 0;
+  // steps per batched dB / dC reduction (the fused-epilogue build stages more
+  // operands in LDS and keeps a smaller tile, to stay at 2 workgroups per CU)
+  constexpr int kRB = EPI ? 4 : 8;
   static_assert(kCK % kRB == 0, "reduction batches must tile the block");
   constexpr int EB = EPI ? 2 : 1;
   constexpr int ER = EPI ? kCK : 1;
@@ -437,9 +451,13 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
   __shared__ __attribute__((aligned(16))) float s_B[2][kCK][NS];
   __shared__ __attribute__((aligned(16))) float s_C[2][kCK][NS];
   __shared__ float s_sig[2][kCK][kCh];                 // softplus'(delta) = sigmoid(delta) (SSM_DELTA_SOFTPLUS)
-  __shared__ float sbuf[EPI ? 2 : 1][NG][kCK][kWave];  // [du | ddelta] per wave; (gate) y per lane
+  __shared__ float sbuf[NG][kCK][kWave];               // [du | ddelta] per wave
+  __shared__ float ybuf[EPI ? NG : 1][EPI ? kCK : 1][kCh];  // (gate) y of each wave's states, per channel
   __shared__ float bcbuf[2][kCK][NS];                  // dB, dC totals of this channel block
   __shared__ float bdummy[2][kWave];                   // sink for lanes without a total
+  // per wave: the dB (or dC) values of kRB steps, one row of 32 channels per
+  // (step, state slot, half), summed row-wise every kRB steps
+  __shared__ __attribute__((aligned(16))) float rbuf[NG][kRB * 4][kRS];
 
   const int64_t bLD = (int64_t)b * L * D;
   const int64_t bLN = (int64_t)b * L * N;
@@ -495,19 +513,28 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
 #pragma unroll
     for (int j = 0; j < 2; ++j) r_h[j] = ld32(ck_b, (uint32_t)((blk * N + min(n0 + j, N - 1)) * D + dc));
   };
-  auto commit = [&](int buf, int blk) {
-    const int t0 = blk * kCK;
+  // softplus(delta) and its derivative: a separate copy of the staging loop
+  auto stage_dt = [&](int buf, int t0, auto sp_tag) {
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
       const int i = srow0 + k * RSTEP;
       const bool in = svalid && t0 + i < L;
-      s_u[buf][i][scol] = in ? r_u[k] : 0.0f;
-      if (dsp) {
+      if constexpr (decltype(sp_tag)::value) {
         s_dt[buf][i][scol] = in ? softplus(r_dt[k]) : 0.0f;
         s_sig[buf][i][scol] = in ? sigmoid(r_dt[k]) : 0.0f;
       } else {
         s_dt[buf][i][scol] = in ? r_dt[k] : 0.0f;
       }
+    }
+  };
+  auto commit = [&](int buf, int blk) {
+    const int t0 = blk * kCK;
+    if (dsp) stage_dt(buf, t0, std::true_type{}); else stage_dt(buf, t0, std::false_type{});
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      const int i = srow0 + k * RSTEP;
+      const bool in = svalid && t0 + i < L;
+      s_u[buf][i][scol] = in ? r_u[k] : 0.0f;
       const float go = in ? r_dy[k] : 0.0f;
       if (gate) {
         const float gz = in ? r_gz[k] : 0.0f;
@@ -562,11 +589,47 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
           dyv[i] = s_dy[buf][i][c];
         }
       }
-      // dB / dC values of kRB consecutive steps (8 per lane) are summed over
-      // each wave half together; one lane per quad writes each total, the
-      // others write a per-lane dummy slot
-      float xb[kRB][2];
-      auto flush = [&](int i0, int qsel) {
+      // dB / dC: lane (c, hf) writes its two values of step i into rows
+      // ((i % kRB) * 2 + slot) * 2 + hf of its wave's tile.  When a batch of
+      // kRB steps is written, lane l reads its part of row l % kRows with
+      // float4 loads; two steps later it sums them, the parts are added across
+      // lanes, and lanes < kRows write the totals (the others a per-lane dummy
+      // slot).  LDS operations of one wave execute in order and the compiler
+      // keeps the tile's (possibly aliasing) writes and reads in program
+      // order, so no barrier or wait is needed between them.
+      // B_t and C_t are read kPF steps ahead of use, before the tile writes
+      // of the steps in between, so their latency is covered as well.
+      float(*tile)[kRS] = rbuf[wave];
+      auto put = [&](int i, float v0, float v1) {
+        tile[((i % kRB) * 2 + 0) * 2 + hf][c] = v0;
+        tile[((i % kRB) * 2 + 1) * 2 + hf][c] = v1;
+      };
+      constexpr int kRows = kRB * 4;            // 32 or 16 rows
+      constexpr int kPer = 32 * kRows / kWave;  // values of a row per lane: 16 or 8
+      float4 pq[kPer / 4];
+      auto flush_issue = [&]() {
+        const float4* src = reinterpret_cast<const float4*>(&tile[lane % kRows][kPer * (lane / kRows)]);
+#pragma unroll
+        for (int k = 0; k < kPer / 4; ++k) pq[k] = src[k];
+      };
+      auto flush_finish = [&](int i0, int qsel) {
+        float v = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kPer / 4; ++k) v += (pq[k].x + pq[k].y) + (pq[k].z + pq[k].w);
+        if constexpr (kRows == 16) {  // lanes l, l ^ 16 hold parts of one row
+          auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+          v = __uint_as_float(s16[0]) + __uint_as_float(s16[1]);
+        }
+        auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        const int r = lane % kRows;
+        const int n = wave * kSPW + 2 * (r & 1) + ((r >> 1) & 1);
+        float* dst = lane < kRows ? &bcbuf[qsel][i0 + (r >> 2)][n] : &bdummy[qsel][lane];
+        *dst = v;
+      };
+      // register path: 4 steps x 2 states summed together with cross-lane moves
+      float xb[4][2];
+      auto xflush = [&](int i0, int qsel) {
         float x8[8];
 #pragma unroll
         for (int m = 0; m < 8; ++m) x8[m] = xb[m >> 1][m & 1];
@@ -576,47 +639,79 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
         float* dst = (lane & 3) == 0 ? &bcbuf[qsel][i0 + (v >> 1)][n] : &bdummy[qsel][lane];
         *dst = r;
       };
+      // steps ahead that B / C are read (the fused-epilogue build has fewer
+      // registers to spare)
+      constexpr int kPF = EPI ? 1 : 2;
+      float2 Bl[kCK], Cl[kCK];
+      auto ldB = [&](int i) { Bl[i] = *reinterpret_cast<const float2*>(&s_B[buf][i][n0]); };
+      auto ldC = [&](int i) { Cl[i] = *reinterpret_cast<const float2*>(&s_C[buf][i][n0]); };
+      float yp[kCK];  // (gate) this lane's part of y, per step
       // forward recompute of the block: a_t, h_{t-1}; dC_t = sum_d dy_t h_t
 #pragma unroll
-      for (int i = 0; i < kCK; ++i) {
-        if (i % kRB == 0) {
+      for (int i = 0; i < kPF; ++i) {
+        ldB(i);
+        if (gate) ldC(i);
+      }
 #pragma unroll
-          for (int bi = 0; bi < kRB; ++bi) xb[bi][0] = xb[bi][1] = 0.0f;
+      for (int i = 0; i < kCK; ++i) {
+        if (i + kPF < kCK) {
+          ldB(i + kPF);
+          if (gate) ldC(i + kPF);
         }
         if (kFull || i < tn) {
-          const float2 Bv = *reinterpret_cast<const float2*>(&s_B[buf][i][n0]);
           const float w = dd[i] * uu[i];
-          const float Bn[2] = {Bv.x, Bv.y};
+          const float Bn[2] = {Bl[i].x, Bl[i].y};
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
             const float a = fast_exp2(A2[j] * dd[i]);
             a_s[i][j] = a;
             hp_s[i][j] = h[j];
             h[j] = fmaf(a, h[j], Bn[j] * w);
-            xb[i % kRB][j] = dyv[i] * h[j];
+          }
+          if constexpr (kDcLds) {
+            put(i, dyv[i] * h[0], dyv[i] * h[1]);
+          } else {
+            xb[i % 4][0] = dyv[i] * h[0];
+            xb[i % 4][1] = dyv[i] * h[1];
           }
           if (gate) {
-            const float2 Cv = *reinterpret_cast<const float2*>(&s_C[buf][i][n0]);
-            sbuf[EPI ? 1 : 0][wave][i][lane] = fmaf(Cv.y, h[1], Cv.x * h[0]);
+            yp[i] = fmaf(Cl[i].y, h[1], Cl[i].x * h[0]);
+            // steps i-1, i: the halves' sums land in lanes < 32 (even step) and >= 32 (odd);
+            // a partial block's last step, if even, is paired with nothing
+            if (i & 1) {
+              ybuf[EPI ? wave : 0][EPI ? i - 1 + hf : 0][c] = half_pair(yp[i - 1], yp[i]);
+            } else if (!kFull && i == tn - 1) {
+              ybuf[EPI ? wave : 0][EPI ? i + hf : 0][c] = half_pair(yp[i], 0.0f);
+            }
           }
         }
-        if (i % kRB == kRB - 1 && (kFull || i - (kRB - 1) < tn)) flush(i - (kRB - 1), 1);
+        // batches are flushed whole: a partial block's rows beyond tn give totals nobody reads
+        if constexpr (kDcLds) {
+          if (i % kRB == kRB - 1) flush_issue();
+          if (i % kRB == 1 && i > kRB) flush_finish(i - 1 - kRB, 1);
+        } else {
+          if (!kFull && i >= tn) xb[i % 4][0] = xb[i % 4][1] = 0.0f;
+          if (i % 4 == 3) xflush(i - 3, 1);
+        }
       }
       // adjoint, backwards through the block
       float dAblk[2] = {0.0f, 0.0f};
 #pragma unroll
-      for (int i = kCK - 1; i >= 0; --i) {
-        if (i % kRB == kRB - 1) {
+      for (int i = 0; i < kPF; ++i) {
+        ldB(kCK - 1 - i);
+        ldC(kCK - 1 - i);
+      }
 #pragma unroll
-          for (int bi = 0; bi < kRB; ++bi) xb[bi][0] = xb[bi][1] = 0.0f;
+      for (int i = kCK - 1; i >= 0; --i) {
+        if (i >= kPF) {
+          ldB(i - kPF);
+          ldC(i - kPF);
         }
         if (kFull || i < tn) {
-          const float2 Bv = *reinterpret_cast<const float2*>(&s_B[buf][i][n0]);
-          const float2 Cv = *reinterpret_cast<const float2*>(&s_C[buf][i][n0]);
-          const float Bn[2] = {Bv.x, Bv.y};
-          const float Cn[2] = {Cv.x, Cv.y};
+          const float Bn[2] = {Bl[i].x, Bl[i].y};
+          const float Cn[2] = {Cl[i].x, Cl[i].y};
           const float w = dd[i] * uu[i];
-          float s1 = 0.0f, s2 = 0.0f;
+          float s1 = 0.0f, s2 = 0.0f, fw[2];
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
             const float f = fmaf(Cn[j], dyv[i], g[j]);
@@ -625,14 +720,30 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
             s2 = fmaf(Av[j], qv, s2);
             dAblk[j] = fmaf(dd[i], qv, dAblk[j]);
             s1 = fmaf(Bn[j], f, s1);
-            xb[i % kRB][j] = f * w;
+            fw[j] = f * w;
             g[j] = gg;
           }
+          if constexpr (kDbLds) {
+            put(i, fw[0], fw[1]);
+          } else {
+            xb[i % 4][0] = fw[0];
+            xb[i % 4][1] = fw[1];
+          }
           // du partial in lanes < 32, ddelta partial in lanes >= 32
-          sbuf[0][wave][i][lane] = half_pair(dd[i] * s1, fmaf(uu[i], s1, s2));
+          sbuf[wave][i][lane] = half_pair(dd[i] * s1, fmaf(uu[i], s1, s2));
         }
-        if (i % kRB == 0 && (kFull || i < tn)) flush(i, 0);
+        if constexpr (kDcLds) {
+          if (i == kCK - 3) flush_finish(kCK - kRB, 1);  // the forward sweep's last dC batch
+        }
+        if constexpr (kDbLds) {
+          if (i % kRB == 0) flush_issue();
+          if (i % kRB == kRB - 2 && i < kCK - kRB) flush_finish(i + 2, 0);
+        } else {
+          if (!kFull && i >= tn) xb[i % 4][0] = xb[i % 4][1] = 0.0f;
+          if (i % 4 == 0) xflush(i, 0);
+        }
       }
+      if constexpr (kDbLds) flush_finish(0, 0);
       dAmid[0] += dAblk[0];
       dAmid[1] += dAblk[1];
     };
@@ -650,8 +761,8 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
           float du = 0.0f, ddt = 0.0f;
 #pragma unroll
           for (int w = 0; w < NG; ++w) {
-            du += sbuf[0][w][i][scol];
-            ddt += sbuf[0][w][i][kCh + scol];
+            du += sbuf[w][i][scol];
+            ddt += sbuf[w][i][kCh + scol];
           }
           const int t = t0 + i;
           const float uu = s_u[buf][i][scol];
@@ -674,7 +785,7 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
           if (gate && svalid) {
             float ys = 0.0f;
 #pragma unroll
-            for (int w = 0; w < NG; ++w) ys += sbuf[EPI ? 1 : 0][w][i][scol] + sbuf[EPI ? 1 : 0][w][i][kCh + scol];
+            for (int w = 0; w < NG; ++w) ys += ybuf[EPI ? w : 0][EPI ? i : 0][scol];
             if (skip) ys = fmaf(stage_eu ? s_eu[buf][i][scol] : uu, Dq, ys);
             const float zz = s_gz[buf][i][scol];
             const float sg = sigmoid(zz);
@@ -817,12 +928,21 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_agg_k
       r_C[k] = ld32(C_b, (uint32_t)min(gi, LN - 1));
     }
   };
-  auto commit = [&](int buf, int t0) {
+  auto stage_dt = [&](int buf, int t0, auto sp_tag) {
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
       const int i = srow0 + k * RSTEP;
       const bool in = svalid && t0 + i < L;
-      s_dt[buf][i][scol] = in ? (dsp ? softplus(r_dt[k]) : r_dt[k]) : 0.0f;
+      const float v = decltype(sp_tag)::value ? softplus(r_dt[k]) : r_dt[k];
+      s_dt[buf][i][scol] = in ? v : 0.0f;
+    }
+  };
+  auto commit = [&](int buf, int t0) {
+    if (dsp) stage_dt(buf, t0, std::true_type{}); else stage_dt(buf, t0, std::false_type{});
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      const int i = srow0 + k * RSTEP;
+      const bool in = svalid && t0 + i < L;
       const float go = in ? r_dy[k] : 0.0f;
       if (gate) {
         const float gz = in ? r_gz[k] : 0.0f;
@@ -1021,10 +1141,15 @@ int launch_fwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const voi
   if (!dispatch_variant(s, [&](auto ng, auto epi) {
         constexpr int G = decltype(ng)::value;
         constexpr bool E = decltype(epi)::value;
-        if (s.nseg > 1)  // aggregates of every segment but the last
-          hipLaunchKernelGGL((ssm_fwd_kernel<G, false, true, T>), dim3(s.ncb, s.B, s.nseg - 1), dim3(kWave * G), 0,
+        auto go = [&](auto sp) {
+          constexpr bool SP = decltype(sp)::value;
+          if (s.nseg > 1)  // aggregates of every segment but the last
+            hipLaunchKernelGGL((ssm_fwd_kernel<G, false, true, SP, T>), dim3(s.ncb, s.B, s.nseg - 1),
+                               dim3(kWave * G), 0, st, a);
+          hipLaunchKernelGGL((ssm_fwd_kernel<G, E, false, SP, T>), dim3(s.ncb, s.B, s.nseg), dim3(kWave * G), 0,
                              st, a);
-        hipLaunchKernelGGL((ssm_fwd_kernel<G, E, false, T>), dim3(s.ncb, s.B, s.nseg), dim3(kWave * G), 0, st, a);
+        };
+        if (desc->flags & SSM_DELTA_SOFTPLUS) go(std::true_type{}); else go(std::false_type{});
       }))
     return fail(SSM_ERR_UNSUPPORTED, "no kernel variant for this shape");
   return hip_check(hipGetLastError(), "ssm_fwd launch");
