@@ -51,6 +51,9 @@ constexpr int kCh = 32;   // channels per workgroup (lane & 31)
 constexpr int kSPW = 4;   // states per wave: 2 per lane, the two lane halves differ
 constexpr int kTT = 32;   // forward time tile
 constexpr int kCK = 16;   // checkpoint interval = backward block length
+#ifndef SSM_FWD_PF
+#define SSM_FWD_PF 2
+#endif
 #ifndef SSM_LDS_DB
 #define SSM_LDS_DB 1
 #endif
@@ -267,12 +270,24 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kerne
           }
         }
       } else {
+        // B_t, C_t read FPF steps ahead of use, before the y writes in between
+        constexpr int FPF = SSM_FWD_PF;
+        float2 Bl[kTT], Cl[kTT];
+#pragma unroll
+        for (int i = 0; i < FPF; ++i) {
+          Bl[i] = *reinterpret_cast<const float2*>(&s_B[buf][i][n0]);
+          Cl[i] = *reinterpret_cast<const float2*>(&s_C[buf][i][n0]);
+        }
 #pragma unroll
         for (int i = 0; i < kTT; ++i) {
+          if (FPF > 0 && i + FPF < kTT) {
+            Bl[i + FPF] = *reinterpret_cast<const float2*>(&s_B[buf][i + FPF][n0]);
+            Cl[i + FPF] = *reinterpret_cast<const float2*>(&s_C[buf][i + FPF][n0]);
+          }
           ys[i] = 0.0f;
           if (kFull || i < tn) {
-            const float2 Bv = *reinterpret_cast<const float2*>(&s_B[buf][i][n0]);
-            const float2 Cv = *reinterpret_cast<const float2*>(&s_C[buf][i][n0]);
+            const float2 Bv = FPF > 0 ? Bl[i] : *reinterpret_cast<const float2*>(&s_B[buf][i][n0]);
+            const float2 Cv = FPF > 0 ? Cl[i] : *reinterpret_cast<const float2*>(&s_C[buf][i][n0]);
             if (ck_b != nullptr && (i % kCK) == 0) {
               const int blk = (t0 + i) / kCK;
 #pragma unroll
