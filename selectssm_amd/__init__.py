@@ -8,6 +8,7 @@ There is no CPU fallback.
 """
 from .conv import conv1d_act
 from .modules import BidirectionalMamba, SelectiveSSM
+from .rcps import RCPSEmbedding, RCPSLMHead, RCPSNorm, RCPSWrapper
 from .scan import (
     SelectiveScanFn,
     largest_factor_up_to,
@@ -20,6 +21,10 @@ from .scan import (
 
 __all__ = [
     "BidirectionalMamba",
+    "RCPSEmbedding",
+    "RCPSLMHead",
+    "RCPSNorm",
+    "RCPSWrapper",
     "SelectiveSSM",
     "SelectiveScanFn",
     "conv1d_act",
