@@ -10,7 +10,8 @@
  *     allocates, never synchronises and only enqueues work on `stream`
  *     (a hipStream_t passed as void*; NULL means the legacy default stream).
  *   - Tensor layouts are the reference's: u, delta, y, z, dy, du, ddelta: (B,L,D)
- *     row-major; A, dA: (D,N); Bc, Cc, dB, dC: (B,L,N); Dskip, dD: (D,).
+ *     row-major (y, dy and z may have a longer row, desc.ld_y / ld_z);
+ *     A, dA: (D,N); Bc, Cc, dB, dC: (B,L,N); Dskip, dD: (D,).
  *     delta may be (B,L,1) (desc.delta_broadcast=1, selectssm.py:36, 203-210).
  *   - I/O element type is desc.dtype (f32 or bf16).  A, Dskip, dA, dD and the
  *     checkpoints are always f32; the recurrent state and every accumulator
@@ -29,7 +30,7 @@
 extern "C" {
 #endif
 
-#define SSM_ABI_VERSION 2
+#define SSM_ABI_VERSION 3
 
 /* error codes */
 #define SSM_OK 0
@@ -62,6 +63,12 @@ typedef struct ssm_desc {
                              (a row's time axis is split into this many segments that run
                              in parallel, joined by their carries; results agree with 1
                              segment up to fp32 rounding) */
+  int64_t ld_y;           /* elements between consecutive time rows of y and dy; 0 = dim.
+                             With ld_y > dim, y is a column slice of a (B, L, ld_y) array
+                             (batch stride L*ld_y), e.g. one half of BidirectionalMamba's
+                             concatenated output (selectssm.py:335-336) */
+  int64_t ld_z;           /* the same for z, e.g. z read in place from in_proj's output
+                             (selectssm.py:319-321); 0 = dim.  dz is always (B,L,D) */
 } ssm_desc_t;
 
 /* Version of this ABI (SSM_ABI_VERSION). */
@@ -142,6 +149,9 @@ typedef struct ssm_conv_desc {
   int32_t dtype;          /* SSM_F32 or SSM_BF16 for x, u, du, dx; w and dw are f32 */
   uint32_t flags;         /* SSM_REVERSE | SSM_COMPLEMENT */
   int32_t activation;     /* SSM_ACT_* */
+  int64_t ld_x;           /* elements between consecutive time rows of x; 0 = dim (x may be a
+                             column slice of in_proj's output, selectssm.py:319); dx is always
+                             (B,L,D) */
 } ssm_conv_desc_t;
 
 /* Bytes of scratch `workspace` that ssm_conv_bwd needs (per-tile dw partial

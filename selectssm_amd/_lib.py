@@ -28,7 +28,7 @@ SSM_ACT_NONE = 0
 SSM_ACT_SILU = 1
 SSM_ACT_RELU = 2
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # every symbol include/selectssm.h declares
 EXPORTS = (
@@ -57,6 +57,8 @@ class SsmDesc(ctypes.Structure):
         ("flags", ctypes.c_uint32),
         ("delta_broadcast", ctypes.c_int32),
         ("segments", ctypes.c_int32),
+        ("ld_y", ctypes.c_int64),
+        ("ld_z", ctypes.c_int64),
     ]
 
 
@@ -71,6 +73,7 @@ class SsmConvDesc(ctypes.Structure):
         ("dtype", ctypes.c_int32),
         ("flags", ctypes.c_uint32),
         ("activation", ctypes.c_int32),
+        ("ld_x", ctypes.c_int64),
     ]
 
 
@@ -134,9 +137,10 @@ def check(code: int) -> None:
         raise SsmError(code, lib().ssm_last_error().decode())
 
 
-def make_desc(batch, seqlen, dim, dstate, dtype=SSM_F32, flags=0, delta_broadcast=False, segments=0) -> SsmDesc:
+def make_desc(batch, seqlen, dim, dstate, dtype=SSM_F32, flags=0, delta_broadcast=False, segments=0,
+              ld_y=0, ld_z=0) -> SsmDesc:
     return SsmDesc(int(batch), int(seqlen), int(dim), int(dstate), int(dtype), int(flags),
-                   1 if delta_broadcast else 0, int(segments))
+                   1 if delta_broadcast else 0, int(segments), int(ld_y), int(ld_z))
 
 
 def size_query(fn, desc, allow_zero=False) -> int:

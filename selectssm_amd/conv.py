@@ -13,7 +13,7 @@ import ctypes
 import torch
 
 from . import _lib as L
-from .scan import _IO_DTYPES, _ptr, _scratch, _stream
+from .scan import _IO_DTYPES, _ptr, _scratch, _stream, as_rows, row_stride
 
 _ACTS = {None: L.SSM_ACT_NONE, "none": L.SSM_ACT_NONE, "silu": L.SSM_ACT_SILU, "relu": L.SSM_ACT_RELU}
 
@@ -32,7 +32,10 @@ def _conv_desc(x, K, reverse, complement, activation):
         flags |= L.SSM_REVERSE
         if complement:
             flags |= L.SSM_COMPLEMENT
-    return L.SsmConvDesc(Bt, Ln, D, int(K), _IO_DTYPES[x.dtype], flags, _act_code(activation))
+    ld = row_stride(x)
+    if ld is None:
+        raise ValueError("x must be contiguous or a column slice of a contiguous (B, L, W) tensor")
+    return L.SsmConvDesc(Bt, Ln, D, int(K), _IO_DTYPES[x.dtype], flags, _act_code(activation), ld)
 
 
 def _weight(w, D):
@@ -43,9 +46,9 @@ def _weight(w, D):
 
 
 def conv_fwd(x, w, reverse=False, complement=False, activation="silu"):
-    """u = act(conv(x_s, w)) in the scan domain (``ssm_conv_fwd``)."""
+    """u = act(conv(x_s, w)) in the scan domain (``ssm_conv_fwd``); x may be a row-strided slice."""
     desc = _conv_desc(x, w.shape[0], reverse, complement, activation)
-    u = torch.empty_like(x)
+    u = torch.empty(x.shape, dtype=x.dtype, device=x.device)
     L.check(L.lib().ssm_conv_fwd(_stream(), ctypes.byref(desc), _ptr(x), _ptr(w), _ptr(u)))
     return u
 
@@ -54,7 +57,7 @@ def conv_bwd(x, w, du, reverse=False, complement=False, activation="silu", need_
     """(dx, dw) of :func:`conv_fwd` (``ssm_conv_bwd``); either may be skipped (None)."""
     desc = _conv_desc(x, w.shape[0], reverse, complement, activation)
     lib = L.lib()
-    dx = torch.empty_like(x) if need_dx else None
+    dx = torch.empty(x.shape, dtype=x.dtype, device=x.device) if need_dx else None
     dw = torch.empty_like(w) if need_dw else None
     ws = _scratch(L.size_query(lib.ssm_conv_bwd_workspace_bytes, desc), x.device) if need_dw else None
     L.check(lib.ssm_conv_bwd(_stream(), ctypes.byref(desc), _ptr(x), _ptr(w), _ptr(du), _ptr(dx), _ptr(dw),
@@ -96,4 +99,4 @@ def conv1d_act(x, w, reverse=False, complement=False, activation="silu"):
         complement = False  # the reference only looks at complement when reverse (selectssm.py:116, 167-168)
     _act_code(activation)
     w = _weight(w, x.shape[-1]).to(torch.float32).contiguous()
-    return ConvActFn.apply(x.contiguous(), w, bool(reverse), bool(complement), activation)
+    return ConvActFn.apply(as_rows(x, x.dtype)[0], w, bool(reverse), bool(complement), activation)

@@ -44,6 +44,7 @@ struct ConvArgs {
   T* dx;
   float* ws_dw;  // [B][ntile][K][D] (backward, when dw is wanted)
   int L, D, ntile;
+  int ldx;  // row stride of x (dx is always (B,L,D))
   bool rev, comp;
   int act;
 };
@@ -73,9 +74,9 @@ __global__ void __launch_bounds__(kLanes* kCW) conv_fwd_kernel(ConvArgs<T> p) {
   const int t0 = (blockIdx.y * kCW + wave) * kCT;           // scan-domain time
   if (d >= D || t0 >= L) return;
   const int q = p.comp ? D - 1 - d : d;                     // channel of x
-  const int64_t base = (int64_t)blockIdx.z * L * D;
-  const T* __restrict__ xb = p.x + base;
-  T* __restrict__ ub = p.u + base;
+  const int ldx = p.ldx;
+  const T* __restrict__ xb = p.x + (int64_t)blockIdx.z * L * ldx;
+  T* __restrict__ ub = p.u + (int64_t)blockIdx.z * L * D;
   float wk[K];
 #pragma unroll
   for (int k = 0; k < K; ++k) wk[k] = p.w[(int64_t)k * D + d];
@@ -85,7 +86,7 @@ __global__ void __launch_bounds__(kLanes* kCW) conv_fwd_kernel(ConvArgs<T> p) {
   for (int j = 0; j < kCT + K - 1; ++j) {
     const int t = t0 - (K - 1) + j;
     const int r = p.rev ? L - 1 - t : t;
-    xs[j] = (t >= 0 && t < L) ? ld(xb, (int64_t)r * D + q) : 0.0f;
+    xs[j] = (t >= 0 && t < L) ? ld(xb, (int64_t)r * ldx + q) : 0.0f;
   }
 #pragma unroll
   for (int i = 0; i < kCT; ++i) {
@@ -109,8 +110,9 @@ __global__ void __launch_bounds__(kLanes* kCW) conv_bwd_kernel(ConvArgs<T> p) {
   const bool live = d < D && t0 < L;
   const int dc = d < D ? d : D - 1;
   const int q = p.comp ? D - 1 - dc : dc;
+  const int ldx = p.ldx;
   const int64_t base = (int64_t)blockIdx.z * L * D;
-  const T* __restrict__ xb = p.x + base;
+  const T* __restrict__ xb = p.x + (int64_t)blockIdx.z * L * ldx;
   const T* __restrict__ dub = p.du + base;
   float wk[K];
 #pragma unroll
@@ -122,7 +124,7 @@ __global__ void __launch_bounds__(kLanes* kCW) conv_bwd_kernel(ConvArgs<T> p) {
   for (int j = 0; j < kCT + 2 * K - 2; ++j) {
     const int t = t0 - (K - 1) + j;
     const int r = p.rev ? L - 1 - t : t;
-    xs[j] = (live && t >= 0 && t < L) ? ld(xb, (int64_t)r * D + q) : 0.0f;
+    xs[j] = (live && t >= 0 && t < L) ? ld(xb, (int64_t)r * ldx + q) : 0.0f;
   }
 #pragma unroll
   for (int j = 0; j < kCT + K - 1; ++j) {
@@ -184,7 +186,7 @@ __global__ void conv_reduce_kernel(const float* __restrict__ ws, float* __restri
 }
 
 struct ConvShape {
-  int B, L, D, K, ntile;
+  int B, L, D, K, ntile, ldx;
 };
 
 int validate_conv(const ssm_conv_desc_t* desc, ConvShape* s) {
@@ -204,6 +206,10 @@ int validate_conv(const ssm_conv_desc_t* desc, ConvShape* s) {
   s->L = (int)desc->seqlen;
   s->D = (int)desc->dim;
   s->K = desc->ksize;
+  if (desc->ld_x != 0 && desc->ld_x < desc->dim) return fail(SSM_ERR_INVALID, "ld_x must be 0 or >= dim");
+  if (desc->seqlen * (desc->ld_x ? desc->ld_x : desc->dim) > (int64_t(1) << 31) - 1)
+    return fail(SSM_ERR_INVALID, "seqlen*ld_x must be < 2^31");
+  s->ldx = desc->ld_x ? (int)desc->ld_x : s->D;
   s->ntile = (s->L + kCT * kCW - 1) / (kCT * kCW);
   if (s->ntile > 65535) return fail(SSM_ERR_INVALID, "seqlen must be <= 65535*128");
   return SSM_OK;
@@ -230,6 +236,7 @@ ConvArgs<T> conv_args(const ssm_conv_desc_t* desc, const ConvShape& s) {
   a.L = s.L;
   a.D = s.D;
   a.ntile = s.ntile;
+  a.ldx = s.ldx;
   a.rev = (desc->flags & SSM_REVERSE) != 0;
   a.comp = (desc->flags & SSM_COMPLEMENT) != 0;
   a.act = desc->activation;

@@ -78,6 +78,7 @@ struct FwdArgs {
   float* agg_H;  // [B][nseg][N][D]: state at the end of each segment from a zero start
   float* agg_S;  // [B][nseg][D]: sum of delta over each segment
   int L, D, N, nblk;
+  int ldy, ldz;       // row strides (elements) of y and z
   int seg_len, nseg;  // time segments per row (seg_len a multiple of kTT)
   int dstride;        // 1, or 0 for a (B,L,1) delta
   uint32_t flags;
@@ -178,10 +179,11 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kerne
   const int scol_dt = p.dstride ? sdc : 0;
   const T* __restrict__ u_b = p.u + bLD;
   const T* __restrict__ dt_b = p.delta + bLDt;
-  const T* __restrict__ z_b = EPI ? p.z + bLD : nullptr;
+  const int ldy = p.ldy, ldz = p.ldz;
+  const T* __restrict__ z_b = EPI ? p.z + (int64_t)b * L * ldz : nullptr;
   const T* __restrict__ B_b = p.Bc + bLN;
   const T* __restrict__ C_b = p.Cc + bLN;
-  T* __restrict__ y_b = p.y + bLD;
+  T* __restrict__ y_b = p.y + (int64_t)b * L * ldy;
   float* __restrict__ ck_b = p.ckpt != nullptr ? p.ckpt + (int64_t)b * p.nblk * N * D : nullptr;
   const int LN = L * N;
   const int ND = N * D;
@@ -199,7 +201,7 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kerne
       if (stage_eu || gate) {
         const int pr = rev ? L - 1 - tc : tc;
         if (stage_eu) r_eu[k] = ld32(u_b, (uint32_t)(pr * D + sq));
-        if (gate) r_ez[k] = ld32(z_b, (uint32_t)(pr * D + sq));
+        if (gate) r_ez[k] = ld32(z_b, (uint32_t)(pr * ldz + sq));
       }
     }
 #pragma unroll
@@ -328,7 +330,7 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kerne
               const float zz = s_ez[buf][i][scol];
               ys *= zz * sigmoid(zz);
             }
-            on_valid_lanes(full_cb, svalid, [&] { st32(y_b, (uint32_t)(pt * D + sq), ys); });
+            on_valid_lanes(full_cb, svalid, [&] { st32(y_b, (uint32_t)(pt * ldy + sq), ys); });
           }
         }
       };
@@ -370,6 +372,7 @@ struct BwdArgs {
   float* agg_G;   // [B][nseg][N][D]: adjoint carry leaving each segment (leftwards) from a zero start
   float* agg_S;   // [B][nseg][D]: sum of delta over each segment
   int Bt, L, D, N, nblk, ncb;
+  int ldy, ldz;   // row strides (elements) of dy and of z
   int seg_len, nseg;
   int dstride;
   uint32_t flags;
@@ -481,8 +484,9 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
   const int scol_dt = p.dstride ? sdc : 0;
   const T* __restrict__ u_b = p.u + bLD;
   const T* __restrict__ dt_b = p.delta + bLDt;
-  const T* __restrict__ dy_b = p.dy + bLD;
-  const T* __restrict__ z_b = EPI ? p.z + bLD : nullptr;
+  const int ldy = p.ldy, ldz = p.ldz;
+  const T* __restrict__ dy_b = p.dy + (int64_t)b * L * ldy;
+  const T* __restrict__ z_b = EPI ? p.z + (int64_t)b * L * ldz : nullptr;
   const T* __restrict__ B_b = p.Bc + bLN;
   const T* __restrict__ C_b = p.Cc + bLN;
   const float* __restrict__ ck_b = p.ckpt + (int64_t)b * p.nblk * N * D;
@@ -503,12 +507,12 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
       const int pr = rev ? L - 1 - tc : tc;  // output row of scan step tc
       r_u[k] = ld32(u_b, (uint32_t)(tc * D + sdc));
       r_dt[k] = ld32(dt_b, (uint32_t)(tc * dtD + scol_dt));
-      r_dy[k] = ld32(dy_b, (uint32_t)(pr * D + sq));
-      if (gate) r_gz[k] = ld32(z_b, (uint32_t)(pr * D + sq));
+      r_dy[k] = ld32(dy_b, (uint32_t)(pr * ldy + sq));
+      if (gate) r_gz[k] = ld32(z_b, (uint32_t)(pr * ldz + sq));
       if (stage_eu) r_eu[k] = ld32(u_b, (uint32_t)(pr * D + sq));
       if (stage_dyo) {
-        r_dyo[k] = ld32(dy_b, (uint32_t)(tc * D + sdc));
-        if (gate) r_zo[k] = ld32(z_b, (uint32_t)(tc * D + sdc));
+        r_dyo[k] = ld32(dy_b, (uint32_t)(tc * ldy + sdc));
+        if (gate) r_zo[k] = ld32(z_b, (uint32_t)(tc * ldz + sdc));
       }
     }
 #pragma unroll
@@ -915,8 +919,9 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_agg_k
   const int dtD = p.dstride ? D : 1;
   const int scol_dt = p.dstride ? sdc : 0;
   const T* __restrict__ dt_b = p.delta + (int64_t)b * L * dtD;
-  const T* __restrict__ dy_b = p.dy + bLD;
-  const T* __restrict__ z_b = EPI ? p.z + bLD : nullptr;
+  const int ldy = p.ldy, ldz = p.ldz;
+  const T* __restrict__ dy_b = p.dy + (int64_t)b * L * ldy;
+  const T* __restrict__ z_b = EPI ? p.z + (int64_t)b * L * ldz : nullptr;
   const T* __restrict__ C_b = p.Cc + bLN;
   const int LN = L * N;
 
@@ -927,8 +932,8 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_agg_k
       const int tc = min(t0 + srow0 + k * RSTEP, L - 1);
       const int pr = rev ? L - 1 - tc : tc;
       r_dt[k] = ld32(dt_b, (uint32_t)(tc * dtD + scol_dt));
-      r_dy[k] = ld32(dy_b, (uint32_t)(pr * D + sq));
-      if (gate) r_gz[k] = ld32(z_b, (uint32_t)(pr * D + sq));
+      r_dy[k] = ld32(dy_b, (uint32_t)(pr * ldy + sq));
+      if (gate) r_gz[k] = ld32(z_b, (uint32_t)(pr * ldz + sq));
     }
 #pragma unroll
     for (int k = 0; k < BCE; ++k) {
@@ -1032,6 +1037,7 @@ struct Shape {
   int NG;    // waves per workgroup (4 states each)
   bool epi;  // skip / gate epilogue fused
   int seg_len, nseg;  // time segments per row
+  int ldy, ldz;       // row strides of y / dy and of z
 };
 
 // Automatic time split: a row is split only when the unsplit grid would leave
@@ -1075,11 +1081,18 @@ int validate(const ssm_desc_t* desc, Shape* s) {
   if (desc->delta_broadcast != 0 && desc->delta_broadcast != 1)
     return fail(SSM_ERR_INVALID, "delta_broadcast must be 0 or 1");
   if (desc->segments < 0 || desc->segments > kMaxSeg) return fail(SSM_ERR_INVALID, "segments must be in 0..1024");
+  if ((desc->ld_y != 0 && desc->ld_y < desc->dim) || (desc->ld_z != 0 && desc->ld_z < desc->dim))
+    return fail(SSM_ERR_INVALID, "ld_y and ld_z must be 0 or >= dim");
+  if ((desc->ld_y != 0 && desc->seqlen * desc->ld_y > (int64_t(1) << 30)) ||
+      (desc->ld_z != 0 && desc->seqlen * desc->ld_z > (int64_t(1) << 30)))
+    return fail(SSM_ERR_INVALID, "seqlen*ld_y and seqlen*ld_z must be <= 2^30");
   s->B = (int)desc->batch;
   s->L = (int)desc->seqlen;
   s->D = (int)desc->dim;
   s->N = (int)desc->dstate;
   s->ncb = (s->D + kCh - 1) / kCh;
+  s->ldy = desc->ld_y ? (int)desc->ld_y : s->D;
+  s->ldz = desc->ld_z ? (int)desc->ld_z : s->D;
   s->nblk = (s->L + kCK - 1) / kCK;
   s->epi = (desc->flags & (SSM_SKIP | SSM_GATE)) != 0;
   const int ng = (s->N + kSPW - 1) / kSPW;
@@ -1151,6 +1164,8 @@ int launch_fwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const voi
   a.nblk = s.nblk;
   a.seg_len = s.seg_len;
   a.nseg = s.nseg;
+  a.ldy = s.ldy;
+  a.ldz = s.ldz;
   a.dstride = desc->delta_broadcast ? 0 : 1;
   a.flags = desc->flags;
   if (!dispatch_variant(s, [&](auto ng, auto epi) {
@@ -1206,6 +1221,8 @@ int launch_bwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const voi
   a.ncb = s.ncb;
   a.seg_len = s.seg_len;
   a.nseg = s.nseg;
+  a.ldy = s.ldy;
+  a.ldz = s.ldz;
   a.dstride = bcast ? 0 : 1;
   a.flags = desc->flags;
   if (!dispatch_variant(s, [&](auto ng, auto epi) {

@@ -10,7 +10,9 @@ The hot path is fused:
   * flip + ``shift_conv`` + activation  -> one ``ssm_conv_fwd`` launch
   * softplus(dt), the scan, the un-flip, the D skip (with the reference's
     flipped-domain ``u``), and in BidirectionalMamba the silu gate
-                                        -> one ``ssm_fwd`` launch
+                                        -> one ``ssm_fwd`` launch per direction,
+    both writing straight into the concatenated output; the conv inputs and the
+    gates are read in place from in_proj's output
   * the Dense projections (BC, dt, dt_proj, in_proj, out_proj) run on hipBLASLt
     through torch.
 Every strategy flag (chunked / ``recursive_scan`` / ``custom_vjp_scan``) runs the
@@ -29,7 +31,7 @@ import torch
 import torch.nn.functional as F
 
 from .conv import conv1d_act
-from .scan import _check_recursion, resolve_chunking, selective_scan
+from .scan import _check_recursion, bidirectional_selective_scan, resolve_chunking, selective_scan
 
 _FUSED_CONV_ACTS = ("silu", "relu", None)
 
@@ -190,10 +192,9 @@ class SelectiveSSM(_FlaxModule):
     def _sow(self, col, name, value):
         self.sown.setdefault(col, {})[name] = value
 
-    def forward(self, x: torch.Tensor, train: bool = False, gate: Optional[torch.Tensor] = None,
-                gate_activation: str = "silu") -> torch.Tensor:
-        """y (B, L, D) for x (B, L, D).  ``gate`` (BidirectionalMamba's z) multiplies the
-        output by gate_activation(z) (selectssm.py:335-336), fused into the scan for silu."""
+    def _prepare(self, x: torch.Tensor) -> dict:
+        """Everything of __call__ before the scan (selectssm.py:156-228): the scan's
+        operands in the scan domain, with delta before its softplus."""
         if self.features is None:
             self._build(x.shape[-1], x.device)
         B, L, D = x.shape
@@ -224,6 +225,9 @@ class SelectiveSSM(_FlaxModule):
         BC = self.BC(u)
         Bc, Cc = BC[..., :N], BC[..., N:]
         dt = self.dt(u)
+        if coeffs:
+            self._sow("diagnostics", "dt_lowrank_mean", dt.mean())
+            self._sow("diagnostics", "dt_lowrank_sd", dt.std(unbiased=False))
         if self.dt_proj_enabled:
             dt = self.dt_proj(dt)
         elif self.rank > 1:
@@ -231,7 +235,6 @@ class SelectiveSSM(_FlaxModule):
                 raise ValueError(f"dt_rank={self.rank} must divide D={D}")
             dt = torch.repeat_interleave(dt, D // self.rank, dim=-1)
         if coeffs:
-            self._sow("diagnostics", "dt_lowrank_mean", self.dt(u).mean())
             dsp = F.softplus(dt)
             for k, v in (("activated_conv_mean", u.mean()), ("activated_conv_sd", u.std(unbiased=False)),
                          ("dt_mean", dsp.mean()), ("dt_sd", dsp.std(unbiased=False)), ("A_mean", A.mean()),
@@ -244,21 +247,45 @@ class SelectiveSSM(_FlaxModule):
             _check_recursion(self.min_recursion_length, self.recursive_split)
         else:
             resolve_chunking(L, D, self.chunk_size, self.n_channel_groups)
+        return dict(u=u, delta=dt, A=A, B=Bc, C=Cc, D=self.D)
 
-        fuse_gate = gate is not None and gate_activation == "silu"
-        y = selective_scan(u, dt, A, Bc, Cc, D=self.D, z=gate if fuse_gate else None, reverse=self.reverse,
-                           complement=self.complement, delta_softplus=True)
-        if gate is not None and not fuse_gate:
-            y = y * _activation_fn(gate_activation)(gate)
+    def _unfused_outputs(self) -> bool:
+        """Diagnostics that sow values the fused epilogue never materialises."""
+        d = self.diagnostics
+        return bool(d) and ("ssm_residual" in d or "ssm_output_norm" in d)
 
+    def _finish(self, y_pre_gate: Optional[torch.Tensor]) -> None:
         if self.regularize:
             kernels = [self.BC.kernel, self.dt.kernel] + ([self.dt_proj.kernel] if self.dt_proj_enabled else [])
             reg = (self.shift_l2_scale * torch.sum(self.shift_conv.kernel ** 2)
                    + self.ssm_l2_scale * sum(torch.sum(k ** 2) for k in kernels))
             self._sow("losses", "ssm_regularizer", reg)
-        if diag and "ssm_output_norm" in diag:
-            self._sow("diagnostics", "ssm_output_mean", y.mean())
-            self._sow("diagnostics", "ssm_output_sd", y.std(unbiased=False))
+        if y_pre_gate is not None and self.diagnostics and "ssm_output_norm" in self.diagnostics:
+            self._sow("diagnostics", "ssm_output_mean", y_pre_gate.mean())
+            self._sow("diagnostics", "ssm_output_sd", y_pre_gate.std(unbiased=False))
+
+    def forward(self, x: torch.Tensor, train: bool = False, gate: Optional[torch.Tensor] = None,
+                gate_activation: str = "silu") -> torch.Tensor:
+        """y (B, L, D) for x (B, L, D).  ``gate`` (BidirectionalMamba's z) multiplies the
+        output by gate_activation(z) (selectssm.py:335-336), fused into the scan for silu."""
+        p = self._prepare(x)
+        u = p["u"]
+        if self._unfused_outputs():
+            # the scan without its epilogue, so the residual and pre-gate values exist
+            y = selective_scan(u, p["delta"], p["A"], p["B"], p["C"], reverse=self.reverse,
+                               complement=self.complement, delta_softplus=True)
+            if "ssm_residual" in self.diagnostics:
+                self._sow("diagnostics", "ssm_residual_mean", y.mean())
+                self._sow("diagnostics", "ssm_residual_sd", y.std(unbiased=False))
+            y = y + u * self.D  # u stays in the scan domain (selectssm.py:238)
+            self._finish(y)
+            return y if gate is None else y * _activation_fn(gate_activation)(gate)
+        fuse_gate = gate is not None and gate_activation == "silu"
+        y = selective_scan(u, p["delta"], p["A"], p["B"], p["C"], D=p["D"], z=gate if fuse_gate else None,
+                           reverse=self.reverse, complement=self.complement, delta_softplus=True)
+        if gate is not None and not fuse_gate:
+            y = y * _activation_fn(gate_activation)(gate)
+        self._finish(None)
         return y
 
 
@@ -415,10 +442,21 @@ class BidirectionalMamba(_FlaxModule):
         zf, _zr = h[..., n_in * ED:(n_in + 1) * ED], h[..., (n_in + 1) * ED:]
         xr = xf if self.tie_in_proj else _xr
         zr = zf if self.tie_gate else _zr
-        # the gate of selectssm.py:335-336 is applied inside each SSM's scan epilogue
-        yf = self.ssm_fwd(xf, train, gate=zf, gate_activation=self.activation)
-        yr = self.ssm_rev(xr, train, gate=zr, gate_activation=self.activation)
-        x = torch.cat([yf, yr], dim=-1) if self.concatenate_fwd_rev else yf + yr
+        # the gate of selectssm.py:335-336 is applied inside each SSM's scan
+        # epilogue; xf, xr, zf, zr are read in place from in_proj's output
+        if (self.concatenate_fwd_rev and self.activation == "silu" and not self.ssm_fwd._unfused_outputs()
+                and not self.ssm_rev._unfused_outputs()):
+            pf = self.ssm_fwd._prepare(xf)
+            pr = self.ssm_rev._prepare(xr)
+            pf["z"], pr["z"] = zf, zr
+            # both directions straight into the concatenated output (selectssm.py:335)
+            x = bidirectional_selective_scan(pf, pr, complement=self.complement, delta_softplus=True)
+            self.ssm_fwd._finish(None)
+            self.ssm_rev._finish(None)
+        else:
+            yf = self.ssm_fwd(xf, train, gate=zf, gate_activation=self.activation)
+            yr = self.ssm_rev(xr, train, gate=zr, gate_activation=self.activation)
+            x = torch.cat([yf, yr], dim=-1) if self.concatenate_fwd_rev else yf + yr
         x = self.out_proj(x)
         x = skip + x
         if self.mlp_layer:

@@ -109,10 +109,32 @@ def _flags(skip, gate, reverse, complement, delta_softplus=False):
     return f
 
 
-def _desc(u, delta, A, flags, segments=0):
+def _desc(u, delta, A, flags, segments=0, ld_y=0, ld_z=0):
     Bt, Ln, D = u.shape
     return L.make_desc(Bt, Ln, D, A.shape[1], _IO_DTYPES[u.dtype], flags,
-                       delta_broadcast=(delta.shape[-1] == 1 and D != 1), segments=segments)
+                       delta_broadcast=(delta.shape[-1] == 1 and D != 1), segments=segments, ld_y=ld_y, ld_z=ld_z)
+
+
+def row_stride(t):
+    """Row stride (elements between time rows) if ``t`` (B, L, D) is a column slice of a
+    contiguous (B, L, W) array -- the layout the kernels read in place -- else None."""
+    if t is None or t.dim() != 3 or t.stride(-1) != 1:
+        return None
+    Bt, Ln, D = t.shape
+    ld = t.stride(1)
+    if ld < D or (Bt > 1 and t.stride(0) != Ln * ld):
+        return None
+    return ld
+
+
+def as_rows(t, dtype):
+    """``t`` in ``dtype`` as a row-strided view the kernels can read, copying only if needed."""
+    if t is None:
+        return None, 0
+    if t.dtype == dtype and row_stride(t) is not None:
+        return t, row_stride(t)
+    t = t.to(dtype).contiguous()
+    return t, t.shape[-1]
 
 
 def _scratch(nbytes, device):
@@ -122,18 +144,22 @@ def _scratch(nbytes, device):
 # ------------------------------------------------------------- raw launchers
 
 def scan_fwd(u, delta, A, B, C, Dskip=None, z=None, reverse=False, complement=False, want_ckpt=True,
-             segments=0, delta_softplus=False):
-    """Run ``ssm_fwd``.  All tensors contiguous, on one GPU, I/O dtype shared.
+             segments=0, delta_softplus=False, y_out=None):
+    """Run ``ssm_fwd``.  Tensors on one GPU, I/O dtype shared; u, delta, B, C contiguous,
+    ``z`` and ``y_out`` contiguous or row-strided column slices (:func:`row_stride`).
 
     ``segments`` splits each row's time axis (0: chosen from the shape);
     ``delta_softplus``: ``delta`` is the pre-activation and the scan uses
-    softplus(delta).  Returns ``(y, ckpt)``; ``ckpt`` is None when
-    ``want_ckpt`` is False.
+    softplus(delta); ``y_out``: where to write y (allocated if None).
+    Returns ``(y, ckpt)``; ``ckpt`` is None when ``want_ckpt`` is False.
     """
     flags = _flags(Dskip is not None, z is not None, reverse, complement, delta_softplus)
-    desc = _desc(u, delta, A, flags, segments)
+    y = torch.empty_like(u) if y_out is None else y_out
+    ld_y, ld_z = row_stride(y), (row_stride(z) if z is not None else 0)
+    if ld_y is None or ld_z is None:
+        raise ValueError("y_out and z must be contiguous or column slices of a contiguous (B, L, W) tensor")
+    desc = _desc(u, delta, A, flags, segments, ld_y=ld_y, ld_z=ld_z)
     lib = L.lib()
-    y = torch.empty_like(u)
     ckpt = _scratch(L.size_query(lib.ssm_ckpt_bytes, desc), u.device) if want_ckpt else None
     ws = _scratch(L.size_query(lib.ssm_fwd_workspace_bytes, desc, allow_zero=True), u.device)
     L.check(lib.ssm_fwd(_stream(), ctypes.byref(desc), _ptr(u), _ptr(delta), _ptr(A), _ptr(B), _ptr(C),
@@ -144,9 +170,13 @@ def scan_fwd(u, delta, A, B, C, Dskip=None, z=None, reverse=False, complement=Fa
 def scan_bwd(u, delta, A, B, C, Dskip, z, ckpt, dy, reverse=False, complement=False, segments=0,
              delta_softplus=False):
     """Run ``ssm_bwd``.  Returns ``(du, ddelta, dA, dB, dC, dD, dz)`` (dD / dz None when unused);
-    with ``delta_softplus``, ``ddelta`` is the gradient w.r.t. the pre-activation."""
+    with ``delta_softplus``, ``ddelta`` is the gradient w.r.t. the pre-activation.
+    ``dy`` and ``z`` may be row-strided column slices; dz is always contiguous."""
     flags = _flags(Dskip is not None, z is not None, reverse, complement, delta_softplus)
-    desc = _desc(u, delta, A, flags, segments)
+    ld_y, ld_z = row_stride(dy), (row_stride(z) if z is not None else 0)
+    if ld_y is None or ld_z is None:
+        raise ValueError("dy and z must be contiguous or column slices of a contiguous (B, L, W) tensor")
+    desc = _desc(u, delta, A, flags, segments, ld_y=ld_y, ld_z=ld_z)
     lib = L.lib()
     du = torch.empty_like(u)
     ddelta = torch.empty_like(delta)
@@ -186,7 +216,7 @@ class SelectiveScanFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy):
         u, delta, A, B, C, Dskip, z, ckpt = ctx.saved_tensors
-        dy = dy.to(u.dtype).contiguous()
+        dy, _ = as_rows(dy, u.dtype)
         du, ddelta, dA, dB, dC, dD, dz = scan_bwd(u, delta, A, B, C, Dskip, z, ckpt, dy, *ctx.flags,
                                                   segments=ctx.segments, delta_softplus=ctx.delta_softplus)
         return du, ddelta, dA, dB, dC, dD, dz, None, None, None, None
@@ -218,8 +248,58 @@ def selective_scan(u, delta, A, B, C, D=None, z=None, reverse=False, complement=
     fcast = lambda t: None if t is None else t.to(torch.float32).contiguous()
     if not 0 <= int(segments) <= 1024:
         raise ValueError(f"segments must be in 0..1024, got {segments}")
-    return SelectiveScanFn.apply(cast(u), cast(delta), fcast(A), cast(B), cast(C), fcast(D), cast(z),
+    return SelectiveScanFn.apply(cast(u), cast(delta), fcast(A), cast(B), cast(C), fcast(D), as_rows(z, io)[0],
                                  bool(reverse), bool(complement), int(segments), bool(delta_softplus))
+
+
+class BidirectionalScanFn(torch.autograd.Function):
+    """The two scans of BidirectionalMamba (forward direction, and reverse with the
+    optional complement) written straight into the concatenated (B, L, 2D) output,
+    each with its D skip and silu(z) gate fused (selectssm.py:325-336)."""
+
+    @staticmethod
+    def forward(ctx, uf, dtf, Af, Bf, Cf, Df, zf, ur, dtr, Ar, Br, Cr, Dr, zr, complement, delta_softplus):
+        Bt, Ln, D = uf.shape
+        y = torch.empty(Bt, Ln, 2 * D, dtype=uf.dtype, device=uf.device)
+        want = torch.is_grad_enabled() or any(ctx.needs_input_grad)
+        _, ckf = scan_fwd(uf, dtf, Af, Bf, Cf, Df, zf, False, False, want_ckpt=want, delta_softplus=delta_softplus,
+                          y_out=y[..., :D])
+        _, ckr = scan_fwd(ur, dtr, Ar, Br, Cr, Dr, zr, True, complement, want_ckpt=want,
+                          delta_softplus=delta_softplus, y_out=y[..., D:])
+        ctx.save_for_backward(uf, dtf, Af, Bf, Cf, Df, zf, ckf, ur, dtr, Ar, Br, Cr, Dr, zr, ckr)
+        ctx.cfg = (complement, delta_softplus)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        uf, dtf, Af, Bf, Cf, Df, zf, ckf, ur, dtr, Ar, Br, Cr, Dr, zr, ckr = ctx.saved_tensors
+        complement, dsp = ctx.cfg
+        D = uf.shape[-1]
+        dy, _ = as_rows(dy, uf.dtype)
+        gf = scan_bwd(uf, dtf, Af, Bf, Cf, Df, zf, ckf, dy[..., :D], False, False, delta_softplus=dsp)
+        gr = scan_bwd(ur, dtr, Ar, Br, Cr, Dr, zr, ckr, dy[..., D:], True, complement, delta_softplus=dsp)
+        return (*gf, *gr, None, None)
+
+
+def bidirectional_selective_scan(fwd, rev, complement=False, delta_softplus=False):
+    """concat([scan_f(...) , scan_r(...)], -1) for BidirectionalMamba in one output buffer.
+
+    ``fwd`` / ``rev``: dicts with u, delta, A, B, C, D, z of each direction (the
+    reverse direction's in its scan domain, as for :func:`selective_scan` with
+    ``reverse=True``).  z may be a column slice of in_proj's output (read in place).
+    """
+    io = _io_dtype(fwd["u"], fwd["delta"], fwd["B"], fwd["C"], fwd["z"], rev["u"], rev["delta"], rev["B"],
+                   rev["C"], rev["z"])
+    cast = lambda t: None if t is None else t.to(io).contiguous()
+    fcast = lambda t: None if t is None else t.to(torch.float32).contiguous()
+    args = []
+    for d in (fwd, rev):
+        _check_shapes(d["u"], d["delta"], d["A"], d["B"], d["C"], d.get("D"), d.get("z"))
+        args += [cast(d["u"]), cast(d["delta"]), fcast(d["A"]), cast(d["B"]), cast(d["C"]), fcast(d.get("D")),
+                 as_rows(d.get("z"), io)[0]]
+    if fwd["u"].shape != rev["u"].shape:
+        raise ValueError("the two directions must have the same (B, L, D)")
+    return BidirectionalScanFn.apply(*args, bool(complement), bool(delta_softplus))
 
 
 # ------------------------------------------------------- reference-named API

@@ -36,7 +36,7 @@ def test_header_constants_match_binding():
               "SSM_ACT_NONE", "SSM_ACT_SILU", "SSM_ACT_RELU"):
         assert int(consts[k]) == getattr(L, k), k
     assert int(consts["SSM_ABI_VERSION"]) == L.ABI_VERSION
-    assert ctypes.sizeof(L.SsmDesc) == 48
+    assert ctypes.sizeof(L.SsmDesc) == 64
 
 
 def test_size_queries():
@@ -88,7 +88,8 @@ def test_split_forward_needs_its_workspace():
 @pytest.mark.parametrize("field,value,msg", [
     ("batch", 0, b"batch, seqlen and dim"), ("dstate", 0, b"dstate"), ("dtype", 7, b"dtype"),
     ("flags", 32, b"unknown flag"), ("flags", 2, b"COMPLEMENT requires"), ("delta_broadcast", 3, b"delta_broadcast"),
-    ("segments", -1, b"segments"), ("segments", 1025, b"segments"),
+    ("segments", -1, b"segments"), ("segments", 1025, b"segments"), ("ld_y", 63, b"ld_y"), ("ld_z", 1, b"ld_z"),
+    ("ld_y", 1 << 28, b"seqlen*ld_y"),
 ])
 def test_invalid_desc_is_rejected_before_any_launch(field, value, msg):
     lib = L.lib()
@@ -116,7 +117,7 @@ def test_null_pointers_and_missing_epilogue_operands_are_rejected():
 
 def test_conv_desc_validation():
     lib = L.lib()
-    assert ctypes.sizeof(L.SsmConvDesc) == 40
+    assert ctypes.sizeof(L.SsmConvDesc) == 48
     p = ctypes.c_void_p(16)
     good = dict(batch=2, seqlen=64, dim=64, ksize=4, dtype=L.SSM_F32, flags=0, activation=L.SSM_ACT_SILU)
     d = L.SsmConvDesc(**good)
@@ -124,7 +125,7 @@ def test_conv_desc_validation():
     assert lib.ssm_conv_bwd_workspace_bytes(ctypes.byref(d)) == 2 * 1 * 4 * 64 * 4
     for field, value, msg in [("ksize", 0, b"ksize"), ("ksize", 9, b"ksize"), ("activation", 3, b"activation"),
                               ("flags", L.SSM_SKIP, b"conv flags"), ("flags", L.SSM_COMPLEMENT, b"COMPLEMENT"),
-                              ("dtype", 5, b"dtype"), ("seqlen", 0, b"seqlen")]:
+                              ("dtype", 5, b"dtype"), ("seqlen", 0, b"seqlen"), ("ld_x", 8, b"ld_x")]:
         bad = L.SsmConvDesc(**{**good, field: value})
         assert lib.ssm_conv_fwd(None, ctypes.byref(bad), p, p, p) == L.SSM_ERR_INVALID, field
         assert msg in lib.ssm_last_error(), (field, lib.ssm_last_error())
