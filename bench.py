@@ -97,6 +97,76 @@ def cpu_baseline(B, L, D, N):
     }
 
 
+MODULES = {
+    1: ("SelectiveSSM(hidden_features=16, shift_conv_size=4, custom_vjp_scan=True) on x (8, 8192, 2048)",
+        dict(kind="ssm", B=8, L=8192, D=2048, kw=dict(custom_vjp_scan=True))),
+    2: ("BidirectionalMamba(hidden_features=16, expansion_factor=2, complement, tie_in_proj, tie_gate, concat), "
+        "d_model 256, on one-hot DNA (4, 131072) embedded by Linear(4, 256)",
+        dict(kind="mamba", B=4, L=131072, D=256)),
+    3: ("SelectiveSSM(hidden_features=16, shift_conv_size=4, recursive_scan=True) on x (1, 1048576, 1024)",
+        dict(kind="ssm", B=1, L=1 << 20, D=1024, kw=dict(recursive_scan=True))),
+    4: ("SelectiveSSM(hidden_features=16, shift_conv_size=4) on bf16 x (16, 4096, 5120)",
+        dict(kind="ssm", B=16, L=4096, D=5120, kw=dict(), bf16=True)),
+}
+
+
+def module_bench(args):
+    """fwd+bwd of the config's whole module (BASELINE.json configs[1..4] module shapes)."""
+    import torch
+    from selectssm_amd import BidirectionalMamba, SelectiveSSM
+
+    desc, m = MODULES[args.config]
+    B, L, D = m["B"], m["L"], m["D"]
+    g = torch.Generator(device="cuda").manual_seed(0)
+    if m["kind"] == "ssm":
+        model = SelectiveSSM(hidden_features=16, shift_conv_size=4, features=D, device="cuda", generator=g, **m["kw"])
+        dtype = torch.bfloat16 if m.get("bf16") else torch.float32
+        x = torch.randn(B, L, D, device="cuda", generator=g).to(dtype)
+        embed = None
+    else:
+        model = BidirectionalMamba(hidden_features=16, expansion_factor=2.0, complement=True, tie_in_proj=True,
+                                   tie_gate=True, concatenate_fwd_rev=True, ssm_args=dict(shift_conv_size=4),
+                                   features=D, device="cuda", generator=g)
+        ids = torch.randint(0, 4, (B, L), device="cuda", generator=g)
+        x = torch.nn.functional.one_hot(ids, 4).float()
+        embed = torch.nn.Linear(4, D, device="cuda")
+    params = list(model.parameters()) + (list(embed.parameters()) if embed is not None else [])
+
+    def step():
+        for p in params:
+            p.grad = None
+        h = embed(x) if embed is not None else x.requires_grad_(True)
+        y = model(h)
+        grad = torch.ones_like(y) if args.config != 2 else torch.randn_like(y, generator=g)
+        y.backward(grad)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return {
+        "metric": "module fwd+bwd tokens/s on 1 MI355X",
+        "value": B * L * args.steps / wall,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": wall * 1e3 / args.steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 I/O, f32 state" if m.get("bf16") else "f32",
+        "data": "synthetic (torch generator, seed 0), random-init parameters",
+        "config": {"workload": desc, "batch": B, "seqlen": L, "d_model" if m["kind"] == "mamba" else "d_inner": D},
+        "peak_hbm_bytes": torch.cuda.max_memory_allocated(),
+    }
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -106,6 +176,9 @@ def main():
     ap.add_argument("--config", type=int, default=1, choices=sorted(CONFIGS),
                     help="BASELINE.json config to run (1 is the bench line)")
     ap.add_argument("--gate", action="store_true", help="fuse the silu(z) gate (BidirectionalMamba epilogue)")
+    ap.add_argument("--module", action="store_true",
+                    help="time the whole module of the config (SelectiveSSM / BidirectionalMamba fwd+bwd, "
+                         "with its projections) instead of the scan op")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (known HBM bytes) to scale rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE counters")
@@ -126,6 +199,10 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy_bytes_read": 4 * n, "calibrate_copy_bytes_written": 4 * n,
                           "launches": max(args.steps, 1)}))
+        return
+
+    if args.module:
+        print(json.dumps(module_bench(args)), flush=True)
         return
 
     from selectssm_amd.scan import scan_bwd, scan_fwd

@@ -85,14 +85,28 @@ __device__ __forceinline__ void on_valid_lanes(bool full_block, bool valid, F&& 
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// 1 / (1 + e^-x): one v_exp_f32 and one v_rcp_f32 (both about 1 ulp)
 __device__ __forceinline__ float sigmoid(float x) {
-  return 1.0f / (1.0f + fast_exp2(-x * kLog2e));
+  return fast_rcp(1.0f + fast_exp2(-x * kLog2e));
+}
+
+// log(1 + y) for y >= 0 as log(u) * y / (u - 1) with u = fl(1 + y): the
+// rounding of 1 + y cancels in the ratio (Goldberg, "What every computer
+// scientist should know about floating-point arithmetic", 1991, Theorem 4);
+// log(u) is v_log_f32 (log2) times ln 2
+__device__ __forceinline__ float log1p_nonneg(float y) {
+  constexpr float kLn2 = 0.6931471805599453f;
+  const float u = 1.0f + y;
+  const float d = u - 1.0f;
+  return d == 0.0f ? y : __builtin_amdgcn_logf(u) * kLn2 * (y * fast_rcp(d));
 }
 
 // softplus(x) = log(1 + e^x) = max(x, 0) + log1p(e^-|x|), as jax.nn.softplus
 // (logaddexp(x, 0)) defines it
 __device__ __forceinline__ float softplus(float x) {
-  return fmaxf(x, 0.0f) + log1pf(fast_exp2(-fabsf(x) * kLog2e));
+  return fmaxf(x, 0.0f) + log1p_nonneg(fast_exp2(-fabsf(x) * kLog2e));
 }
 
 // ------------------------------------------------------ cross-lane reductions

@@ -175,14 +175,29 @@ __global__ void __launch_bounds__(kLanes* kCW) conv_bwd_kernel(ConvArgs<T> p) {
   }
 }
 
-// out[i] = sum_k ws[k*count + i], k = 0..nparts-1 in order
-__global__ void conv_reduce_kernel(const float* __restrict__ ws, float* __restrict__ out, int nparts,
-                                   int64_t count) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= count) return;
+// out[i] = sum over parts k of ws[k*count + i]: a workgroup takes 64
+// consecutive columns; its 16 lane groups sum the parts k = g, g + 16, ... in
+// order, and the 16 group sums are added in order through LDS (a fixed order
+// overall, so dw is deterministic)
+constexpr int kRedCols = 64, kRedGroups = 16;
+__global__ void __launch_bounds__(kRedCols* kRedGroups) conv_reduce_kernel(const float* __restrict__ ws,
+                                                                          float* __restrict__ out, int nparts,
+                                                                          int64_t count) {
+  const int col = threadIdx.x % kRedCols;
+  const int grp = threadIdx.x / kRedCols;
+  const int64_t i = (int64_t)blockIdx.x * kRedCols + col;
   float s = 0.0f;
-  for (int k = 0; k < nparts; ++k) s += ws[(int64_t)k * count + i];
-  out[i] = s;
+  if (i < count)
+    for (int k = grp; k < nparts; k += kRedGroups) s += ws[(int64_t)k * count + i];
+  __shared__ float part[kRedGroups][kRedCols];
+  part[grp][col] = s;
+  __syncthreads();
+  if (grp == 0 && i < count) {
+    float t = 0.0f;
+#pragma unroll
+    for (int g = 0; g < kRedGroups; ++g) t += part[g][col];
+    out[i] = t;
+  }
 }
 
 struct ConvShape {
@@ -275,8 +290,9 @@ int launch_conv_bwd(hipStream_t st, const ssm_conv_desc_t* desc, const ConvShape
   if (int rc = hip_check(hipGetLastError(), "ssm_conv_bwd launch")) return rc;
   if (dw != nullptr) {
     const int64_t count = (int64_t)s.K * s.D;
-    hipLaunchKernelGGL(conv_reduce_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, st,
-                       static_cast<const float*>(workspace), dw, s.B * s.ntile, count);
+    hipLaunchKernelGGL(conv_reduce_kernel, dim3((unsigned)((count + kRedCols - 1) / kRedCols)),
+                       dim3(kRedCols * kRedGroups), 0, st, static_cast<const float*>(workspace), dw, s.B * s.ntile,
+                       count);
     return hip_check(hipGetLastError(), "ssm_conv_bwd reduce launch");
   }
   return SSM_OK;

@@ -124,9 +124,11 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kerne
   const int n0 = wave * kSPW + 2 * hf;  // this lane's states n0, n0 + 1
   const bool rev = p.flags & SSM_REVERSE;
   const bool comp = rev && (p.flags & SSM_COMPLEMENT);
-  const bool skip = EPI && (p.flags & SSM_SKIP);
+  // the skip of a forward scan uses the staged u itself; the reverse skip and
+  // the gate need the extra staging of EPI builds
+  const bool skip = (p.flags & SSM_SKIP) != 0;
   const bool gate = EPI && (p.flags & SSM_GATE);
-  const bool stage_eu = skip && rev;  // u at the output position is another element
+  const bool stage_eu = EPI && skip && rev;  // u at the output position is another element
   // staging / output mapping: thread -> column scol, rows srow0 + k * RSTEP
   const int scol = tid & (kCh - 1);
   const int srow0 = tid / kCh;
@@ -325,7 +327,13 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kerne
             for (int w = 0; w < NG; ++w) ys += s_y[w][i][scol];
             const int t = t0 + i;
             const int pt = rev ? L - 1 - t : t;
-            if (skip) ys = fmaf(stage_eu ? s_eu[buf][i][scol] : s_u[buf][i][scol], Dq, ys);
+            if (skip) {
+              float uo = s_u[buf][i][scol];
+              if constexpr (EPI) {
+                if (stage_eu) uo = s_eu[buf][i][scol];
+              }
+              ys = fmaf(uo, Dq, ys);
+            }
             if (gate) {
               const float zz = s_ez[buf][i][scol];
               ys *= zz * sigmoid(zz);
@@ -414,8 +422,8 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
   const bool rev = p.flags & SSM_REVERSE;
   const bool comp = rev && (p.flags & SSM_COMPLEMENT);
   const bool gate = EPI && (p.flags & SSM_GATE);
-  const bool skip = EPI && (p.flags & SSM_SKIP);
-  const bool stage_dyo = skip && rev;         // gated dy at the unmirrored (t,d) for the skip term
+  const bool skip = (p.flags & SSM_SKIP) != 0;  // non-EPI builds run only the forward-scan skip
+  const bool stage_dyo = EPI && skip && rev;  // gated dy at the unmirrored (t,d) for the skip term
   const bool stage_eu = gate && skip && rev;  // u at the output position for y_pre
   const bool dsp = p.flags & SSM_DELTA_SOFTPLUS;
   const int scol = tid & (kCh - 1);
@@ -788,7 +796,10 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
           if (dsp) ddt *= s_sig[buf][i][scol];  // through softplus (the same factor for every channel when broadcast)
           if (skip) {
             // y_out[t,d] holds u[t,d]*D[d] (selectssm.py:238): its gradient lands on u[t,d]
-            const float dyo = stage_dyo ? s_dyo[buf][i][scol] : s_dy[buf][i][scol];
+            float dyo = s_dy[buf][i][scol];
+            if constexpr (EPI) {
+              if (stage_dyo) dyo = s_dyo[buf][i][scol];
+            }
             du = fmaf(Dd, dyo, du);
             dDblk = fmaf(dyo, uu, dDblk);
           }
@@ -1094,7 +1105,8 @@ int validate(const ssm_desc_t* desc, Shape* s) {
   s->ldy = desc->ld_y ? (int)desc->ld_y : s->D;
   s->ldz = desc->ld_z ? (int)desc->ld_z : s->D;
   s->nblk = (s->L + kCK - 1) / kCK;
-  s->epi = (desc->flags & (SSM_SKIP | SSM_GATE)) != 0;
+  // extra epilogue staging: the gate, and the reverse skip's u at the mirrored position
+  s->epi = (desc->flags & SSM_GATE) || ((desc->flags & SSM_SKIP) && (desc->flags & SSM_REVERSE));
   const int ng = (s->N + kSPW - 1) / kSPW;
   s->NG = 1;
   while (s->NG < ng) s->NG *= 2;  // instantiated wave counts: 1, 2, 4, 8
