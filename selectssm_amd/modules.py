@@ -31,7 +31,8 @@ import torch
 import torch.nn.functional as F
 
 from .conv import conv1d_act
-from .scan import _check_recursion, bidirectional_selective_scan, resolve_chunking, selective_scan
+from .scan import (_check_recursion, as_rows, bidirectional_selective_scan, resolve_chunking, scan_bwd, scan_fwd,
+                   selective_scan)
 
 _FUSED_CONV_ACTS = ("silu", "relu", None)
 
@@ -131,6 +132,64 @@ class _FlaxModule(torch.nn.Module):
         return tree
 
 
+class _SSMCoreFn(torch.autograd.Function):
+    """u -> BC, dt (-> dt_proj) projections -> scan with softplus(dt), D skip and
+    optional silu(z) gate (selectssm.py:190-238), with a hand-written backward
+    that accumulates u's three gradient contributions in place (addmm with
+    beta = 1) instead of separate addition kernels."""
+
+    @staticmethod
+    def forward(ctx, u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, Dp, z, N, rank, reverse, complement):
+        B_, L_, D = u.shape
+        u2 = u.reshape(-1, D)
+        BC = torch.addmm(bbc.to(u.dtype), u2, Wbc.to(u.dtype))
+        dt_low = torch.addmm(bdt.to(u.dtype), u2, Wdt.to(u.dtype))
+        if Wp is not None:
+            dt = torch.addmm(bp.to(u.dtype), dt_low, Wp.to(u.dtype)).reshape(B_, L_, D)
+        elif rank > 1:
+            dt = torch.repeat_interleave(dt_low, D // rank, dim=-1).reshape(B_, L_, D)
+        else:
+            dt = dt_low.reshape(B_, L_, 1)
+        Bc = BC[:, :N].reshape(B_, L_, N).contiguous()
+        Cc = BC[:, N:].reshape(B_, L_, N).contiguous()
+        A = -torch.exp(A_log)
+        y, ckpt = scan_fwd(u, dt.contiguous(), A, Bc, Cc, Dp, z, reverse, complement, delta_softplus=True)
+        ctx.save_for_backward(u, A_log, A, Wbc, Wdt, Wp, Dp, z, dt_low, dt, Bc, Cc, ckpt)
+        ctx.cfg = (N, rank, reverse, complement)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        u, A_log, A, Wbc, Wdt, Wp, Dp, z, dt_low, dt, Bc, Cc, ckpt = ctx.saved_tensors
+        N, rank, reverse, complement = ctx.cfg
+        B_, L_, D = u.shape
+        dy, _ = as_rows(dy, u.dtype)
+        du, ddt, dA, dB, dC, dD, dz = scan_bwd(u, dt.contiguous(), A, Bc, Cc, Dp, z, ckpt, dy, reverse, complement,
+                                               delta_softplus=True)
+        u2 = u.reshape(-1, D)
+        du2 = du.reshape(-1, D)
+        dBC = torch.cat([dB.reshape(-1, N), dC.reshape(-1, N)], dim=1)
+        dWbc = u2.t() @ dBC
+        dbbc = dBC.sum(0)
+        du2.addmm_(dBC, Wbc.to(u.dtype).t())
+        if Wp is not None:
+            ddt2 = ddt.reshape(-1, D)
+            dWp = dt_low.t() @ ddt2
+            dbp = ddt2.sum(0)
+            ddt_low = ddt2 @ Wp.to(u.dtype).t()
+        else:
+            dWp = dbp = None
+            ddt_low = ddt.reshape(-1, D).reshape(-1, rank, D // rank).sum(-1) if rank > 1 else ddt.reshape(-1, 1)
+        dWdt = u2.t() @ ddt_low
+        dbdt = ddt_low.sum(0)
+        du2.addmm_(ddt_low, Wdt.to(u.dtype).t())
+        dA_log = dA * A  # A = -exp(A_log)
+        cast = lambda g, p: None if g is None else g.to(p.dtype)
+        return (du, dA_log, cast(dWbc, Wbc), cast(dbbc, Wbc), cast(dWdt, Wdt), cast(dbdt, Wdt),
+                cast(dWp, Wbc) if Wp is not None else None, cast(dbp, Wbc) if Wp is not None else None, dD, dz,
+                None, None, None, None)
+
+
 class SelectiveSSM(_FlaxModule):
     """A variation on MAMBA (selectssm.py:112-238), on MI355X kernels."""
 
@@ -192,9 +251,14 @@ class SelectiveSSM(_FlaxModule):
     def _sow(self, col, name, value):
         self.sown.setdefault(col, {})[name] = value
 
-    def _prepare(self, x: torch.Tensor) -> dict:
+    def _needs_intermediates(self) -> bool:
+        d = self.diagnostics
+        return bool(d) and any(k in d for k in ("ssm_coeffs", "ssm_residual", "ssm_output_norm"))
+
+    def _prepare(self, x: torch.Tensor, projections: bool = True) -> dict:
         """Everything of __call__ before the scan (selectssm.py:156-228): the scan's
-        operands in the scan domain, with delta before its softplus."""
+        operands in the scan domain, with delta before its softplus (only the conv
+        output u when ``projections`` is False)."""
         if self.features is None:
             self._build(x.shape[-1], x.device)
         B, L, D = x.shape
@@ -220,6 +284,14 @@ class SelectiveSSM(_FlaxModule):
             self._sow("diagnostics", "conv_sd", u.std(unbiased=False))
         if not fused and self.activation is not None:
             u = _activation_fn(self.activation)(u)
+        if not projections:
+            if self.custom_vjp_scan or self.recursive_scan:
+                _check_recursion(self.min_recursion_length, self.recursive_split)
+            else:
+                resolve_chunking(L, D, self.chunk_size, self.n_channel_groups)
+            if not self.dt_proj_enabled and self.rank > 1 and D % self.rank != 0:
+                raise ValueError(f"dt_rank={self.rank} must divide D={D}")
+            return dict(u=u)
 
         A = -torch.exp(self.A_log)
         BC = self.BC(u)
@@ -268,6 +340,14 @@ class SelectiveSSM(_FlaxModule):
                 gate_activation: str = "silu") -> torch.Tensor:
         """y (B, L, D) for x (B, L, D).  ``gate`` (BidirectionalMamba's z) multiplies the
         output by gate_activation(z) (selectssm.py:335-336), fused into the scan for silu."""
+        fuse_gate = gate is not None and gate_activation == "silu"
+        if not self._needs_intermediates():
+            u = self._prepare(x, projections=False)["u"]
+            y = self._core(u, gate if fuse_gate else None)
+            if gate is not None and not fuse_gate:
+                y = y * _activation_fn(gate_activation)(gate)
+            self._finish(None)
+            return y
         p = self._prepare(x)
         u = p["u"]
         if self._unfused_outputs():
@@ -280,13 +360,21 @@ class SelectiveSSM(_FlaxModule):
             y = y + u * self.D  # u stays in the scan domain (selectssm.py:238)
             self._finish(y)
             return y if gate is None else y * _activation_fn(gate_activation)(gate)
-        fuse_gate = gate is not None and gate_activation == "silu"
         y = selective_scan(u, p["delta"], p["A"], p["B"], p["C"], D=p["D"], z=gate if fuse_gate else None,
                            reverse=self.reverse, complement=self.complement, delta_softplus=True)
         if gate is not None and not fuse_gate:
             y = y * _activation_fn(gate_activation)(gate)
         self._finish(None)
         return y
+
+    def _core(self, u: torch.Tensor, z: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Projections + scan from the conv output u in one autograd node (see _SSMCoreFn)."""
+        io = u.dtype
+        zz = None if z is None else as_rows(z, io)[0]
+        return _SSMCoreFn.apply(u, self.A_log, self.BC.kernel, self.BC.bias, self.dt.kernel, self.dt.bias,
+                                self.dt_proj.kernel if self.dt_proj_enabled else None,
+                                self.dt_proj.bias if self.dt_proj_enabled else None, self.D, zz,
+                                self.hidden_features, self.rank, self.reverse, self.complement)
 
 
 class RMSNorm(torch.nn.Module):
