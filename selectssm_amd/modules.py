@@ -132,6 +132,53 @@ class _FlaxModule(torch.nn.Module):
         return tree
 
 
+def _core_forward(u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, Dp, z, N, rank, reverse, complement, y_out=None):
+    """Projections + scan (selectssm.py:190-238); returns (y, saved tensors)."""
+    B_, L_, D = u.shape
+    u2 = u.reshape(-1, D)
+    BC = torch.addmm(bbc.to(u.dtype), u2, Wbc.to(u.dtype))
+    dt_low = torch.addmm(bdt.to(u.dtype), u2, Wdt.to(u.dtype))
+    if Wp is not None:
+        dt = torch.addmm(bp.to(u.dtype), dt_low, Wp.to(u.dtype)).reshape(B_, L_, D)
+    elif rank > 1:
+        dt = torch.repeat_interleave(dt_low, D // rank, dim=-1).reshape(B_, L_, D)
+    else:
+        dt = dt_low.reshape(B_, L_, 1)
+    Bc = BC[:, :N].reshape(B_, L_, N).contiguous()
+    Cc = BC[:, N:].reshape(B_, L_, N).contiguous()
+    A = -torch.exp(A_log)
+    y, ckpt = scan_fwd(u, dt.contiguous(), A, Bc, Cc, Dp, z, reverse, complement, delta_softplus=True, y_out=y_out)
+    return y, (u, A, Wbc, Wdt, Wp, Dp, z, dt_low, dt, Bc, Cc, ckpt)
+
+
+def _core_backward(saved, dy, N, rank, reverse, complement):
+    """Gradients of _core_forward for (u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, D, z)."""
+    u, A, Wbc, Wdt, Wp, Dp, z, dt_low, dt, Bc, Cc, ckpt = saved
+    D = u.shape[-1]
+    du, ddt, dA, dB, dC, dD, dz = scan_bwd(u, dt.contiguous(), A, Bc, Cc, Dp, z, ckpt, dy, reverse, complement,
+                                           delta_softplus=True)
+    u2 = u.reshape(-1, D)
+    du2 = du.reshape(-1, D)
+    dBC = torch.cat([dB.reshape(-1, N), dC.reshape(-1, N)], dim=1)
+    dWbc = u2.t() @ dBC
+    dbbc = dBC.sum(0)
+    du2.addmm_(dBC, Wbc.to(u.dtype).t())  # u's gradient through BC, accumulated in place
+    if Wp is not None:
+        ddt2 = ddt.reshape(-1, D)
+        dWp = (dt_low.t() @ ddt2).to(Wp.dtype)
+        dbp = ddt2.sum(0).to(Wp.dtype)
+        ddt_low = ddt2 @ Wp.to(u.dtype).t()
+    else:
+        dWp = dbp = None
+        ddt_low = ddt.reshape(-1, rank, D // rank).sum(-1) if rank > 1 else ddt.reshape(-1, 1)
+    dWdt = u2.t() @ ddt_low
+    dbdt = ddt_low.sum(0)
+    du2.addmm_(ddt_low, Wdt.to(u.dtype).t())  # and through dt
+    dA_log = dA * A  # A = -exp(A_log)
+    f32 = lambda g: g.to(torch.float32)
+    return du, dA_log, f32(dWbc), f32(dbbc), f32(dWdt), f32(dbdt), dWp, dbp, dD, dz
+
+
 class _SSMCoreFn(torch.autograd.Function):
     """u -> BC, dt (-> dt_proj) projections -> scan with softplus(dt), D skip and
     optional silu(z) gate (selectssm.py:190-238), with a hand-written backward
@@ -140,54 +187,43 @@ class _SSMCoreFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, Dp, z, N, rank, reverse, complement):
-        B_, L_, D = u.shape
-        u2 = u.reshape(-1, D)
-        BC = torch.addmm(bbc.to(u.dtype), u2, Wbc.to(u.dtype))
-        dt_low = torch.addmm(bdt.to(u.dtype), u2, Wdt.to(u.dtype))
-        if Wp is not None:
-            dt = torch.addmm(bp.to(u.dtype), dt_low, Wp.to(u.dtype)).reshape(B_, L_, D)
-        elif rank > 1:
-            dt = torch.repeat_interleave(dt_low, D // rank, dim=-1).reshape(B_, L_, D)
-        else:
-            dt = dt_low.reshape(B_, L_, 1)
-        Bc = BC[:, :N].reshape(B_, L_, N).contiguous()
-        Cc = BC[:, N:].reshape(B_, L_, N).contiguous()
-        A = -torch.exp(A_log)
-        y, ckpt = scan_fwd(u, dt.contiguous(), A, Bc, Cc, Dp, z, reverse, complement, delta_softplus=True)
-        ctx.save_for_backward(u, A_log, A, Wbc, Wdt, Wp, Dp, z, dt_low, dt, Bc, Cc, ckpt)
+        y, saved = _core_forward(u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, Dp, z, N, rank, reverse, complement)
+        ctx.save_for_backward(*saved)
         ctx.cfg = (N, rank, reverse, complement)
         return y
 
     @staticmethod
     def backward(ctx, dy):
-        u, A_log, A, Wbc, Wdt, Wp, Dp, z, dt_low, dt, Bc, Cc, ckpt = ctx.saved_tensors
-        N, rank, reverse, complement = ctx.cfg
-        B_, L_, D = u.shape
-        dy, _ = as_rows(dy, u.dtype)
-        du, ddt, dA, dB, dC, dD, dz = scan_bwd(u, dt.contiguous(), A, Bc, Cc, Dp, z, ckpt, dy, reverse, complement,
-                                               delta_softplus=True)
-        u2 = u.reshape(-1, D)
-        du2 = du.reshape(-1, D)
-        dBC = torch.cat([dB.reshape(-1, N), dC.reshape(-1, N)], dim=1)
-        dWbc = u2.t() @ dBC
-        dbbc = dBC.sum(0)
-        du2.addmm_(dBC, Wbc.to(u.dtype).t())
-        if Wp is not None:
-            ddt2 = ddt.reshape(-1, D)
-            dWp = dt_low.t() @ ddt2
-            dbp = ddt2.sum(0)
-            ddt_low = ddt2 @ Wp.to(u.dtype).t()
-        else:
-            dWp = dbp = None
-            ddt_low = ddt.reshape(-1, D).reshape(-1, rank, D // rank).sum(-1) if rank > 1 else ddt.reshape(-1, 1)
-        dWdt = u2.t() @ ddt_low
-        dbdt = ddt_low.sum(0)
-        du2.addmm_(ddt_low, Wdt.to(u.dtype).t())
-        dA_log = dA * A  # A = -exp(A_log)
-        cast = lambda g, p: None if g is None else g.to(p.dtype)
-        return (du, dA_log, cast(dWbc, Wbc), cast(dbbc, Wbc), cast(dWdt, Wdt), cast(dbdt, Wdt),
-                cast(dWp, Wbc) if Wp is not None else None, cast(dbp, Wbc) if Wp is not None else None, dD, dz,
-                None, None, None, None)
+        dy, _ = as_rows(dy, ctx.saved_tensors[0].dtype)
+        return (*_core_backward(ctx.saved_tensors, dy, *ctx.cfg), None, None, None, None)
+
+
+class _PairCoreFn(torch.autograd.Function):
+    """Both BidirectionalMamba directions' cores (_SSMCoreFn), each writing its y
+    straight into its half of the concatenated output (selectssm.py:325-336)."""
+
+    @staticmethod
+    def forward(ctx, uf, A_logf, Wbcf, bbcf, Wdtf, bdtf, Wpf, bpf, Df, zf,
+                ur, A_logr, Wbcr, bbcr, Wdtr, bdtr, Wpr, bpr, Dr, zr, N, rank, complement):
+        B_, L_, E = uf.shape
+        y = torch.empty(B_, L_, 2 * E, dtype=uf.dtype, device=uf.device)
+        _, sf = _core_forward(uf, A_logf, Wbcf, bbcf, Wdtf, bdtf, Wpf, bpf, Df, zf, N, rank, False, False,
+                              y_out=y[..., :E])
+        _, sr = _core_forward(ur, A_logr, Wbcr, bbcr, Wdtr, bdtr, Wpr, bpr, Dr, zr, N, rank, True, complement,
+                              y_out=y[..., E:])
+        ctx.save_for_backward(*sf, *sr)
+        ctx.cfg = (N, rank, complement, len(sf))
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        N, rank, complement, k = ctx.cfg
+        saved = ctx.saved_tensors
+        E = saved[0].shape[-1]
+        dy, _ = as_rows(dy, saved[0].dtype)
+        gf = _core_backward(saved[:k], dy[..., :E], N, rank, False, False)
+        gr = _core_backward(saved[k:], dy[..., E:], N, rank, True, complement)
+        return (*gf, *gr, None, None, None)
 
 
 class SelectiveSSM(_FlaxModule):
@@ -367,14 +403,16 @@ class SelectiveSSM(_FlaxModule):
         self._finish(None)
         return y
 
+    def _core_args(self, u, z):
+        return (u, self.A_log, self.BC.kernel, self.BC.bias, self.dt.kernel, self.dt.bias,
+                self.dt_proj.kernel if self.dt_proj_enabled else None,
+                self.dt_proj.bias if self.dt_proj_enabled else None, self.D, z)
+
     def _core(self, u: torch.Tensor, z: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Projections + scan from the conv output u in one autograd node (see _SSMCoreFn)."""
-        io = u.dtype
-        zz = None if z is None else as_rows(z, io)[0]
-        return _SSMCoreFn.apply(u, self.A_log, self.BC.kernel, self.BC.bias, self.dt.kernel, self.dt.bias,
-                                self.dt_proj.kernel if self.dt_proj_enabled else None,
-                                self.dt_proj.bias if self.dt_proj_enabled else None, self.D, zz,
-                                self.hidden_features, self.rank, self.reverse, self.complement)
+        zz = None if z is None else as_rows(z, u.dtype)[0]
+        return _SSMCoreFn.apply(*self._core_args(u, zz), self.hidden_features, self.rank, self.reverse,
+                                self.complement)
 
 
 class RMSNorm(torch.nn.Module):
@@ -534,13 +572,21 @@ class BidirectionalMamba(_FlaxModule):
         # epilogue; xf, xr, zf, zr are read in place from in_proj's output
         if (self.concatenate_fwd_rev and self.activation == "silu" and not self.ssm_fwd._unfused_outputs()
                 and not self.ssm_rev._unfused_outputs()):
-            pf = self.ssm_fwd._prepare(xf)
-            pr = self.ssm_rev._prepare(xr)
-            pf["z"], pr["z"] = zf, zr
-            # both directions straight into the concatenated output (selectssm.py:335)
-            x = bidirectional_selective_scan(pf, pr, complement=self.complement, delta_softplus=True)
-            self.ssm_fwd._finish(None)
-            self.ssm_rev._finish(None)
+            f, r = self.ssm_fwd, self.ssm_rev
+            if f._needs_intermediates() or r._needs_intermediates():
+                pf = f._prepare(xf)
+                pr = r._prepare(xr)
+                pf["z"], pr["z"] = zf, zr
+                # both directions straight into the concatenated output (selectssm.py:335)
+                x = bidirectional_selective_scan(pf, pr, complement=self.complement, delta_softplus=True)
+            else:
+                uf = f._prepare(xf, projections=False)["u"]
+                ur = r._prepare(xr, projections=False)["u"]
+                io = uf.dtype
+                x = _PairCoreFn.apply(*f._core_args(uf, as_rows(zf, io)[0]), *r._core_args(ur, as_rows(zr, io)[0]),
+                                      f.hidden_features, f.rank, self.complement)
+            f._finish(None)
+            r._finish(None)
         else:
             yf = self.ssm_fwd(xf, train, gate=zf, gate_activation=self.activation)
             yr = self.ssm_rev(xr, train, gate=zr, gate_activation=self.activation)

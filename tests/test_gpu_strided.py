@@ -114,4 +114,7 @@ def test_bidirectional_mamba_pair_path_equals_per_direction_path():
     yb.square().sum().backward()
     pa, pb = dict(a.named_parameters()), dict(b.named_parameters())
     for k in pa:
-        assert torch.allclose(pa[k].grad, pb[k].grad, rtol=1e-4, atol=1e-6), k
+        # the two paths add u's gradient contributions in different orders; the
+        # weight gradients are sums over B*L terms, so compare at their scale
+        ref = pb[k].grad
+        assert torch.allclose(pa[k].grad, ref, rtol=1e-4, atol=1e-5 * float(ref.abs().max())), k
