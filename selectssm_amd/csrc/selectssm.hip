@@ -51,6 +51,12 @@ constexpr int kCh = 32;   // channels per workgroup (lane & 31)
 constexpr int kSPW = 4;   // states per wave: 2 per lane, the two lane halves differ
 constexpr int kTT = 32;   // forward time tile
 constexpr int kCK = 16;   // checkpoint interval = backward block length
+#ifndef SSM_BWD_RB
+#define SSM_BWD_RB 16
+#endif
+#ifndef SSM_BWD_PF
+#define SSM_BWD_PF 2
+#endif
 #ifndef SSM_FWD_PF
 #define SSM_FWD_PF 2
 #endif
@@ -400,7 +406,7 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
   constexpr bool kDcLds = SSM_LDS_DC != 0;
   // steps per batched dB / dC reduction (the fused-epilogue build stages more
   // operands in LDS and keeps a smaller tile, to stay at 2 workgroups per CU)
-  constexpr int kRB = EPI ? 4 : 8;
+  constexpr int kRB = EPI ? 4 : SSM_BWD_RB;
   static_assert(kCK % kRB == 0, "reduction batches must tile the block");
   constexpr int EB = EPI ? 2 : 1;
   constexpr int ER = EPI ? kCK : 1;
@@ -631,8 +637,8 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
         tile[((i % kRB) * 2 + 0) * 2 + hf][c] = v0;
         tile[((i % kRB) * 2 + 1) * 2 + hf][c] = v1;
       };
-      constexpr int kRows = kRB * 4;            // 32 or 16 rows
-      constexpr int kPer = 32 * kRows / kWave;  // values of a row per lane: 16 or 8
+      constexpr int kRows = kRB * 4;            // 64, 32 or 16 rows
+      constexpr int kPer = 32 * kRows / kWave;  // values of a row per lane: 32, 16 or 8
       float4 pq[kPer / 4];
       auto flush_issue = [&]() {
         const float4* src = reinterpret_cast<const float4*>(&tile[lane % kRows][kPer * (lane / kRows)]);
@@ -647,8 +653,10 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
           auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
           v = __uint_as_float(s16[0]) + __uint_as_float(s16[1]);
         }
-        auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-        v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        if constexpr (kRows < kWave) {  // lanes l, l ^ 32 hold parts of one row
+          auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+          v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        }
         const int r = lane % kRows;
         const int n = wave * kSPW + 2 * (r & 1) + ((r >> 1) & 1);
         float* dst = lane < kRows ? &bcbuf[qsel][i0 + (r >> 2)][n] : &bdummy[qsel][lane];
@@ -668,7 +676,7 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
       };
       // steps ahead that B / C are read (the fused-epilogue build has fewer
       // registers to spare)
-      constexpr int kPF = EPI ? 1 : 2;
+      constexpr int kPF = EPI ? 1 : SSM_BWD_PF;
       float2 Bl[kCK], Cl[kCK];
       auto ldB = [&](int i) { Bl[i] = *reinterpret_cast<const float2*>(&s_B[buf][i][n0]); };
       auto ldC = [&](int i) { Cl[i] = *reinterpret_cast<const float2*>(&s_C[buf][i][n0]); };

@@ -189,3 +189,24 @@ def test_config3_channels_match_c_port(inputs3, split3):
         _close(f"du[{lo}]", g[0][..., sl], gr[0])
         _close(f"ddt[{lo}]", g[1][..., sl], gr[1])
         _close(f"dA[{lo}]", g[2][sl], gr[2])
+
+
+@pytest.mark.parametrize("N", [3, 7, 16, 29], ids=lambda n: f"N{n}")
+@pytest.mark.parametrize("flags", [(), ("reverse", "complement", "skip", "gate", "softplus")], ids=lambda f: "+".join(f) or "plain")
+@pytest.mark.parametrize("segments", [1, 3])
+def test_every_state_count_variant(N, flags, segments):
+    """1, 2, 4 and 8 waves per workgroup (N up to 4, 8, 16, 32), with and without the
+    fused epilogue, unsplit and split, against the fp64 oracle."""
+    print(f"N={N} flags={flags} segments={segments}", flush=True)
+    inp = make_inputs(2, 150, 40, N, seed=20 + N)
+    if "softplus" in flags:
+        inp["dt"] = np.log(np.expm1(inp["dt"].astype(np.float64))).astype(np.float32)
+    y, g = _run(inp, flags, segments=segments)
+    yr, gr = _oracle(inp, flags)
+    _close("y", y, yr)
+    for k in ("u", "dt", "A", "B", "C"):
+        _close(f"d{k}", g[k], gr[k])
+    if "skip" in flags:
+        _close("dD", g["D"], gr["D"])
+    if "gate" in flags:
+        _close("dz", g["z"], gr["z"])
