@@ -83,6 +83,21 @@ __device__ __forceinline__ void on_valid_lanes(bool full_block, bool valid, F&& 
   }
 }
 
+// Whether v holds on any lane of a workgroup of NW waves, with the barrier
+// included: each wave's vote goes to its slot of flags (NW ints of LDS), then
+// every lane reads all slots.  A caller that votes again before the next
+// barrier passes the other half of a double buffer.
+template <int NW>
+__device__ __forceinline__ bool barrier_any(bool v, int* flags) {
+  const bool w = __ballot(v) != 0;
+  if ((threadIdx.x & 63) == 0) flags[threadIdx.x >> 6] = w;
+  __syncthreads();
+  int any = 0;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) any |= flags[i];
+  return any != 0;
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }

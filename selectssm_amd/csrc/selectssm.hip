@@ -6,11 +6,13 @@
 //     holds two workgroups whose barriers are independent.
 //   * rows too few to fill the chip (B * ceil(D/32) small: long-sequence
 //     shapes) are split in time into segments joined by carries: an aggregate
-//     pass gives each segment's (sum of delta, end state from a zero start),
-//     and each segment of the main pass folds the earlier segments' aggregates
-//     into its starting state (the combine of selectssm.py:81-85 applied to
-//     whole segments).  The backward does the same for the adjoint carry,
-//     right to left.
+//     pass gives each segment's (decay product P, end state H from a zero
+//     start), and each segment of the main pass folds the earlier segments'
+//     aggregates into its starting state, h = P h + H (the combine of
+//     selectssm.py:81-85 applied to whole segments).  The backward does the
+//     same for the adjoint carry, right to left.  The aggregate walks flush
+//     products below 2^-126 to zero and stop where every P of the workgroup
+//     is 0, since all further terms are then exact zeros.
 //   * lane = channel: lane l holds channel l & 31, and the two 32-lane halves
 //     of a wave hold different states of the same 32 channels.  Each lane keeps
 //     2 states, a wave 4, and the NG = ceil(N/4) waves of a workgroup all N.
@@ -82,7 +84,7 @@ struct FwdArgs {
   T* y;
   float* ckpt;
   float* agg_H;  // [B][nseg][N][D]: state at the end of each segment from a zero start
-  float* agg_S;  // [B][nseg][D]: sum of delta over each segment
+  float* agg_P;  // [B][nseg][N][D]: product of the segment's decays a_t
   int L, D, N, nblk;
   int ldy, ldz;       // row strides (elements) of y and z
   int seg_len, nseg;  // time segments per row (seg_len a multiple of kTT)
@@ -90,20 +92,15 @@ struct FwdArgs {
   uint32_t flags;
 };
 
-// NG waves (4 states each) per workgroup; EPI: the skip / gate epilogue is
-// fused (its extra staging only exists in EPI builds).  Workgroup
-// (cb, b, seg) scans time segment seg of its rows.
-//   AGG = false: the segment starts from the state the earlier segments hand
-//     over (folded from their aggregates) and writes y and the checkpoints.
-//   AGG = true: aggregate pass for a time-split scan: the segment's state at
-//     its end from a zero start, and its sum of delta, so that
-//     h_end = exp(A * sum delta) * h_start + H (the combine of
-//     selectssm.py:81-85 applied to a whole segment).
+// NG waves (4 states each) per workgroup; EPI: the extra staging of the
+// reverse skip and the gate.  Workgroup (cb, b, seg) scans time segment seg of
+// its rows, starting from the state the earlier segments hand over (folded
+// from their aggregates, ssm_fwd_agg_kernel), and writes y and the
+// checkpoints.
 // SP: delta arrives before softplus (SSM_DELTA_SOFTPLUS); a separate build,
 // because carrying the unused softplus code in the time loop slows it down.
-template <int NG, bool EPI, bool AGG, bool SP, typename T>
+template <int NG, bool EPI, bool SP, typename T>
 __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kernel(FwdArgs<T> p) {
-  static_assert(!(EPI && AGG), "the aggregate pass has no epilogue");
   constexpr int NS = NG * kSPW;         // padded state count
   constexpr int NT = kWave * NG;        // threads
   constexpr int RPT = kTT * kCh / NT;   // staged (step, channel) elements per thread
@@ -152,33 +149,27 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kerne
     A2[j] = (valid && n < N) ? p.A[(int64_t)dc * N + n] * kLog2e : 0.0f;
     h[j] = 0.0f;
   }
-  if (!AGG && seg > 0) {
-    // state entering this segment: fold the earlier segments' aggregates in order
-    const float* __restrict__ aS = p.agg_S + (int64_t)b * p.nseg * D + dc;
-    const float* __restrict__ aH = p.agg_H + (int64_t)b * p.nseg * N * D + dc;
+  if (seg > 0) {
+    // state entering this segment: h = P h + H over the earlier segments in
+    // order (the combine of selectssm.py:81-85 applied to whole segments)
+    const int64_t base = (int64_t)b * p.nseg * N * D + dc;
     const int nc0 = min(n0, N - 1), nc1 = min(n0 + 1, N - 1);
 #pragma unroll 4
     for (int s = 0; s < seg; ++s) {
-      const float sd = aS[(int64_t)s * D];
-      const float H0 = aH[((int64_t)s * N + nc0) * D];
-      const float H1 = aH[((int64_t)s * N + nc1) * D];
-      h[0] = fmaf(fast_exp2(A2[0] * sd), h[0], H0);
-      h[1] = fmaf(fast_exp2(A2[1] * sd), h[1], H1);
+      const int64_t o0 = base + ((int64_t)s * N + nc0) * D, o1 = base + ((int64_t)s * N + nc1) * D;
+      h[0] = fmaf(p.agg_P[o0], h[0], p.agg_H[o0]);
+      h[1] = fmaf(p.agg_P[o1], h[1], p.agg_H[o1]);
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j)
       if (!(valid && n0 + j < N)) h[j] = 0.0f;
   }
-  float dsum = 0.0f;  // AGG: sum of delta over the segment (channel c)
 
-  constexpr int CB = AGG ? 1 : 2;    // the aggregate pass does not stage C
-  constexpr int CR = AGG ? 1 : kTT;
-  constexpr int YG = AGG ? 1 : NG;   // nor y
   __shared__ float s_u[2][kTT][kCh], s_dt[2][kTT][kCh];
   __shared__ float s_eu[EB][ER][kCh], s_ez[EB][ER][kCh];
   __shared__ __attribute__((aligned(16))) float s_B[2][kTT][NS];
-  __shared__ __attribute__((aligned(16))) float s_C[CB][CR][NS];
-  __shared__ float s_y[YG][CR][kCh];
+  __shared__ __attribute__((aligned(16))) float s_C[2][kTT][NS];
+  __shared__ float s_y[NG][kTT][kCh];
 
   const int64_t bLD = (int64_t)b * L * D;
   const int64_t bLN = (int64_t)b * L * N;
@@ -224,7 +215,7 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kerne
       }
       const int gc = min(gi, LN - 1);
       r_B[k] = ld32(B_b, (uint32_t)gc);
-      if (!AGG) r_C[k] = ld32(C_b, (uint32_t)gc);
+      r_C[k] = ld32(C_b, (uint32_t)gc);
     }
   };
   auto commit = [&](int buf, int t0) {
@@ -243,7 +234,7 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kerne
       const int i = e / NS, n = e - (e / NS) * NS;
       const bool in = t0 + i < L && n < N;
       (&s_B[buf][0][0])[e] = in ? r_B[k] : 0.0f;
-      if (!AGG) (&s_C[buf][0][0])[e] = in ? r_C[k] : 0.0f;
+      (&s_C[buf][0][0])[e] = in ? r_C[k] : 0.0f;
     }
   };
 
@@ -268,18 +259,7 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kerne
           dd[i] = s_dt[buf][i][c];
         }
       }
-      if constexpr (AGG) {
-#pragma unroll
-        for (int i = 0; i < kTT; ++i) {
-          if (kFull || i < tn) {
-            const float2 Bv = *reinterpret_cast<const float2*>(&s_B[buf][i][n0]);
-            const float w = dd[i] * uu[i];
-            h[0] = fmaf(fast_exp2(A2[0] * dd[i]), h[0], Bv.x * w);
-            h[1] = fmaf(fast_exp2(A2[1] * dd[i]), h[1], Bv.y * w);
-            dsum += dd[i];
-          }
-        }
-      } else {
+      {
         // B_t, C_t read FPF steps ahead of use, before the y writes in between
         constexpr int FPF = SSM_FWD_PF;
         float2 Bl[kTT], Cl[kTT];
@@ -320,7 +300,7 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kerne
       }
     };
     if (tn == kTT) tile(std::true_type{}); else tile(std::false_type{});
-    if constexpr (!AGG) {
+    {
       __syncthreads();
       auto yreduce = [&](auto full_tag) {
         constexpr bool kFull = decltype(full_tag)::value;
@@ -353,12 +333,158 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kerne
     if (more) commit(buf ^ 1, t0 + kTT);
     __syncthreads();
   }
-  if constexpr (AGG) {
-    const int64_t o = (int64_t)b * p.nseg + seg;
+}
+
+// A segment's running decay product is flushed to zero once it falls below
+// the smallest normal float (2^-126), as in flush-to-zero arithmetic: with
+// subnormals kept, a product whose step factors exceed 1/2 stalls at the
+// smallest subnormal instead of reaching 0.  What the flush drops is below
+// 2^-126 times the later terms; it would matter only if the remaining decays
+// grew by some 2^100 within the segment, which A <= 0, delta >= 0 rule out.
+__device__ __forceinline__ void flush_tiny(float (&P)[2]) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      if (valid && n0 + j < N) p.agg_H[(o * N + n0 + j) * D + d] = h[j];
-    if (wave == 0 && hf == 0 && valid) p.agg_S[o * D + d] = dsum;
+  for (int j = 0; j < 2; ++j) P[j] = P[j] < 0x1p-126f ? 0.0f : P[j];
+}
+
+// Forward aggregate pass of a time-split scan.  Workgroup (cb, b, seg), for
+// segments seg < nseg - 1, writes the segment's state at its end from a zero
+// start, H = sum_t P_t B_t delta_t u_t with P_t the product of the decays
+// after step t, and the whole segment's decay product P.  It walks the segment
+// from its end (H += P B delta u, then P *= a), so once every P of the
+// workgroup is 0 (flushed at tile ends, flush_tiny) all earlier steps add
+// exact zeros and the walk stops there: with decaying states only the last
+// few thousand steps of a long segment are read.
+template <int NG, bool SP, typename T>
+__global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_agg_kernel(FwdArgs<T> p) {
+  constexpr int NS = NG * kSPW;
+  constexpr int NT = kWave * NG;
+  constexpr int RPT = kTT * kCh / NT;
+  constexpr int RSTEP = NT / kCh;
+  constexpr int BCE = kTT * NS / NT;
+  static_assert(BCE * NT == kTT * NS && RPT * NT == kTT * kCh, "staging must tile exactly");
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & (kCh - 1);
+  const int hf = lane >> 5;
+  const int b = blockIdx.y;
+  const int cb = blockIdx.x;
+  const int seg = blockIdx.z;
+  const int L = p.L, D = p.D, N = p.N;
+  const int t_lo = seg * p.seg_len;
+  const int t_hi = min(L, t_lo + p.seg_len);
+  const int d = cb * kCh + c;
+  const bool valid = d < D;
+  const int dc = valid ? d : 0;
+  const int n0 = wave * kSPW + 2 * hf;
+  const int scol = tid & (kCh - 1);
+  const int srow0 = tid / kCh;
+  const int sd = cb * kCh + scol;
+  const bool svalid = sd < D;
+  const int sdc = svalid ? sd : 0;
+
+  float A2[2], H[2] = {0.0f, 0.0f}, P[2] = {1.0f, 1.0f};
+  bool live[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    live[j] = valid && n0 + j < N;
+    A2[j] = live[j] ? p.A[(int64_t)dc * N + n0 + j] * kLog2e : 0.0f;
+  }
+
+  __shared__ float s_u[2][kTT][kCh], s_dt[2][kTT][kCh];
+  __shared__ __attribute__((aligned(16))) float s_B[2][kTT][NS];
+  __shared__ int s_alive[2][NG];
+
+  const int dtD = p.dstride ? D : 1;
+  const int scol_dt = p.dstride ? sdc : 0;
+  const T* __restrict__ u_b = p.u + (int64_t)b * L * D;
+  const T* __restrict__ dt_b = p.delta + (int64_t)b * L * dtD;
+  const T* __restrict__ B_b = p.Bc + (int64_t)b * L * N;
+  const int LN = L * N;
+
+  float r_u[RPT], r_dt[RPT], r_B[BCE];
+  auto fetch = [&](int t0) {
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      const int tc = min(t0 + srow0 + k * RSTEP, L - 1);
+      r_u[k] = ld32(u_b, (uint32_t)(tc * D + sdc));
+      r_dt[k] = ld32(dt_b, (uint32_t)(tc * dtD + scol_dt));
+    }
+#pragma unroll
+    for (int k = 0; k < BCE; ++k) {
+      const int e = tid + k * NT;
+      int gi;
+      if (NS == N) {
+        gi = t0 * N + e;
+      } else {
+        const int i = e / NS, n = e - i * NS;
+        gi = (t0 + i) * N + min(n, N - 1);
+      }
+      r_B[k] = ld32(B_b, (uint32_t)min(gi, LN - 1));
+    }
+  };
+  auto commit = [&](int buf, int t0) {
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      const int i = srow0 + k * RSTEP;
+      const bool in = svalid && t0 + i < L;
+      s_u[buf][i][scol] = in ? r_u[k] : 0.0f;
+      s_dt[buf][i][scol] = in ? (SP ? softplus(r_dt[k]) : r_dt[k]) : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < BCE; ++k) {
+      const int e = tid + k * NT;
+      const int i = e / NS, n = e - (e / NS) * NS;
+      (&s_B[buf][0][0])[e] = (t0 + i < L && n < N) ? r_B[k] : 0.0f;
+    }
+  };
+
+  const int t_last = t_lo + (t_hi - 1 - t_lo) / kTT * kTT;
+  fetch(t_last);
+  commit(0, t_last);
+  __syncthreads();
+  int buf = 0;
+  for (int t0 = t_last;; t0 -= kTT, buf ^= 1) {
+    const bool more = t0 > t_lo;
+    if (more) fetch(t0 - kTT);
+    const int tn = min(kTT, L - t0);
+    auto tile = [&](auto full_tag) {
+      constexpr bool kFull = decltype(full_tag)::value;
+      float uu[kTT], dd[kTT];
+#pragma unroll
+      for (int i = 0; i < kTT; ++i) {
+        if (kFull || i < tn) {
+          uu[i] = s_u[buf][i][c];
+          dd[i] = s_dt[buf][i][c];
+        }
+      }
+#pragma unroll
+      for (int i = kTT - 1; i >= 0; --i) {
+        if (kFull || i < tn) {
+          const float2 Bv = *reinterpret_cast<const float2*>(&s_B[buf][i][n0]);
+          const float w = dd[i] * uu[i];
+          H[0] = fmaf(P[0], Bv.x * w, H[0]);
+          H[1] = fmaf(P[1], Bv.y * w, H[1]);
+          P[0] *= fast_exp2(A2[0] * dd[i]);
+          P[1] *= fast_exp2(A2[1] * dd[i]);
+        }
+      }
+    };
+    if (tn == kTT) tile(std::true_type{}); else tile(std::false_type{});
+    if (more) commit(buf ^ 1, t0 - kTT);
+    // products below the smallest normal float are flushed to zero; every
+    // earlier step then adds an exact zero, so the walk ends once all are 0
+    flush_tiny(P);
+    const bool alive = (live[0] && P[0] != 0.0f) || (live[1] && P[1] != 0.0f);
+    if (!barrier_any<NG>(alive, s_alive[buf]) || !more) break;
+  }
+  const int64_t o = (int64_t)b * p.nseg + seg;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    if (live[j]) {
+      p.agg_H[(o * N + n0 + j) * D + d] = H[j];
+      p.agg_P[(o * N + n0 + j) * D + d] = P[j];
+    }
   }
 }
 
@@ -384,7 +510,7 @@ struct BwdArgs {
   float* ws_dD;   // [B][nseg][D]
   float* ws_ddt;  // [ncb][B][L] (broadcast delta only)
   float* agg_G;   // [B][nseg][N][D]: adjoint carry leaving each segment (leftwards) from a zero start
-  float* agg_S;   // [B][nseg][D]: sum of delta over each segment
+  float* agg_P;   // [B][nseg][N][D]: product of the segment's decays a_t
   int Bt, L, D, N, nblk, ncb;
   int ldy, ldz;   // row strides (elements) of dy and of z
   int seg_len, nseg;
@@ -452,19 +578,16 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
     dAacc[j] = 0.0f;
   }
   if (seg < p.nseg - 1) {
-    // adjoint carry entering this segment from the right: fold the later
-    // segments' aggregates, last segment first (g = a_t f_t at each segment's
-    // first step is linear in the carry it receives)
-    const float* __restrict__ aS = p.agg_S + (int64_t)b * p.nseg * D + dc;
-    const float* __restrict__ aG = p.agg_G + (int64_t)b * p.nseg * N * D + dc;
+    // adjoint carry entering this segment from the right: g = P g + G over the
+    // later segments, last segment first (g = a_t f_t at each segment's first
+    // step is linear in the carry it receives)
+    const int64_t base = (int64_t)b * p.nseg * N * D + dc;
     const int nc0 = min(n0, N - 1), nc1 = min(n0 + 1, N - 1);
 #pragma unroll 4
     for (int s = p.nseg - 1; s > seg; --s) {
-      const float sd = aS[(int64_t)s * D];
-      const float G0 = aG[((int64_t)s * N + nc0) * D];
-      const float G1 = aG[((int64_t)s * N + nc1) * D];
-      g[0] = fmaf(fast_exp2(A2[0] * sd), g[0], G0);
-      g[1] = fmaf(fast_exp2(A2[1] * sd), g[1], G1);
+      const int64_t o0 = base + ((int64_t)s * N + nc0) * D, o1 = base + ((int64_t)s * N + nc1) * D;
+      g[0] = fmaf(p.agg_P[o0], g[0], p.agg_G[o0]);
+      g[1] = fmaf(p.agg_P[o1], g[1], p.agg_G[o1]);
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -882,11 +1005,14 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
 }
 
 // Aggregate pass of a time-split backward.  Workgroup (cb, b, seg - 1), for
-// segments seg >= 1, walks its segment backwards with no carry from the right
-// and writes the carry it hands to the segment on its left, a_t f_t at the
-// segment's first step t (f_t = C_t dy_t + a_{t+1} f_{t+1}, ssmrecscan.py:96-100,
-// 150-153), and the segment's sum of delta.  The carry a segment receives
-// from the right enters that value as exp(A * sum delta) * carry.
+// segments seg >= 1, writes the carry the segment hands to the segment on its
+// left with no carry from the right, G = a_t f_t at the segment's first step t
+// (f_t = C_t dy_t + a_{t+1} f_{t+1}, ssmrecscan.py:96-100, 150-153), i.e.
+// G = sum_t P_t C_t dy_t with P_t the product of the decays up to and including
+// step t, and the whole segment's decay product P, through which a carry from
+// the right enters G.  It walks the segment forwards (P *= a, then G += P C dy),
+// so once every P of the workgroup is 0 (flushed at tile ends, flush_tiny) all
+// later steps add exact zeros and the walk stops there.
 template <int NG, bool EPI, typename T>
 __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_agg_kernel(BwdArgs<T> p) {
   constexpr int NS = NG * kSPW;
@@ -921,17 +1047,17 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_agg_k
   const int sdc = svalid ? sd : 0;
   const int sq = comp ? D - 1 - sdc : sdc;
 
-  float A2[2], g[2];
+  float A2[2], G[2] = {0.0f, 0.0f}, P[2] = {1.0f, 1.0f};
+  bool live[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int n = n0 + j;
-    A2[j] = (valid && n < N) ? p.A[(int64_t)dc * N + n] * kLog2e : 0.0f;
-    g[j] = 0.0f;
+    live[j] = valid && n0 + j < N;
+    A2[j] = live[j] ? p.A[(int64_t)dc * N + n0 + j] * kLog2e : 0.0f;
   }
-  float dsum = 0.0f;
 
   __shared__ float s_dt[2][kTT][kCh], s_dy[2][kTT][kCh];
   __shared__ __attribute__((aligned(16))) float s_C[2][kTT][NS];
+  __shared__ int s_alive[2][NG];
 
   const int64_t bLD = (int64_t)b * L * D;
   const int64_t bLN = (int64_t)b * L * N;
@@ -998,14 +1124,13 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_agg_k
     }
   };
 
-  const int t_last = t_lo + (t_hi - 1 - t_lo) / kTT * kTT;
-  fetch(t_last);
-  commit(0, t_last);
+  fetch(t_lo);
+  commit(0, t_lo);
   __syncthreads();
   int buf = 0;
-  for (int t0 = t_last; t0 >= t_lo; t0 -= kTT, buf ^= 1) {
-    const bool more = t0 > t_lo;
-    if (more) fetch(t0 - kTT);
+  for (int t0 = t_lo;; t0 += kTT, buf ^= 1) {
+    const bool more = t0 + kTT < t_hi;
+    if (more) fetch(t0 + kTT);
     const int tn = min(kTT, L - t0);
     auto tile = [&](auto full_tag) {
       constexpr bool kFull = decltype(full_tag)::value;
@@ -1018,24 +1143,31 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_agg_k
         }
       }
 #pragma unroll
-      for (int i = kTT - 1; i >= 0; --i) {
+      for (int i = 0; i < kTT; ++i) {
         if (kFull || i < tn) {
           const float2 Cv = *reinterpret_cast<const float2*>(&s_C[buf][i][n0]);
-          g[0] = fast_exp2(A2[0] * dd[i]) * fmaf(Cv.x, dyv[i], g[0]);
-          g[1] = fast_exp2(A2[1] * dd[i]) * fmaf(Cv.y, dyv[i], g[1]);
-          dsum += dd[i];
+          P[0] *= fast_exp2(A2[0] * dd[i]);
+          P[1] *= fast_exp2(A2[1] * dd[i]);
+          G[0] = fmaf(P[0], Cv.x * dyv[i], G[0]);
+          G[1] = fmaf(P[1], Cv.y * dyv[i], G[1]);
         }
       }
     };
     if (tn == kTT) tile(std::true_type{}); else tile(std::false_type{});
-    if (more) commit(buf ^ 1, t0 - kTT);
-    __syncthreads();
+    if (more) commit(buf ^ 1, t0 + kTT);
+    // as in the forward aggregate: flushed products end the walk
+    flush_tiny(P);
+    const bool alive = (live[0] && P[0] != 0.0f) || (live[1] && P[1] != 0.0f);
+    if (!barrier_any<NG>(alive, s_alive[buf]) || !more) break;
   }
   const int64_t o = (int64_t)b * p.nseg + seg;
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
-    if (valid && n0 + j < N) p.agg_G[(o * N + n0 + j) * D + d] = g[j];
-  if (wave == 0 && hf == 0 && valid) p.agg_S[o * D + d] = dsum;
+  for (int j = 0; j < 2; ++j) {
+    if (live[j]) {
+      p.agg_G[(o * N + n0 + j) * D + d] = G[j];
+      p.agg_P[(o * N + n0 + j) * D + d] = P[j];
+    }
+  }
 }
 
 // out[i] = sum_k ws[k*count + i], k = 0..nparts-1 in order
@@ -1140,11 +1272,11 @@ bool dispatch_variant(const Shape& s, F&& f) {
 size_t ckpt_floats(const Shape& s) { return (size_t)s.B * s.nblk * s.N * s.D; }
 
 // Per-segment aggregates of a time-split scan: [B][nseg][N][D] states (or
-// adjoint carries) then [B][nseg][D] delta sums.  None for one segment.
-size_t agg_floats(const Shape& s) { return s.nseg > 1 ? (size_t)s.B * s.nseg * (s.N + 1) * s.D : 0; }
+// adjoint carries) then [B][nseg][N][D] decay products.  None for one segment.
+size_t agg_floats(const Shape& s) { return s.nseg > 1 ? (size_t)2 * s.B * s.nseg * s.N * s.D : 0; }
 
 struct WsLayout {
-  size_t dB, dC, dA, dD, ddt, aggG, aggS, total;  // float offsets
+  size_t dB, dC, dA, dD, ddt, aggG, aggP, total;  // float offsets
 };
 
 WsLayout ws_layout(const Shape& s, bool bcast) {
@@ -1157,7 +1289,7 @@ WsLayout ws_layout(const Shape& s, bool bcast) {
   w.dD = w.dA + parts * s.D * s.N;
   w.ddt = w.dD + parts * s.D;
   w.aggG = w.ddt + (bcast ? (size_t)s.ncb * s.B * s.L : 0);
-  w.aggS = w.aggG + (s.nseg > 1 ? parts * s.N * s.D : 0);
+  w.aggP = w.aggG + (s.nseg > 1 ? parts * s.N * s.D : 0);
   w.total = w.aggG + agg_floats(s);
   return w;
 }
@@ -1177,7 +1309,7 @@ int launch_fwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const voi
   a.y = static_cast<T*>(y);
   a.ckpt = ckpt;
   a.agg_H = static_cast<float*>(workspace);
-  a.agg_S = a.agg_H + (s.nseg > 1 ? (size_t)s.B * s.nseg * s.N * s.D : 0);
+  a.agg_P = a.agg_H + (s.nseg > 1 ? (size_t)s.B * s.nseg * s.N * s.D : 0);
   a.L = s.L;
   a.D = s.D;
   a.N = s.N;
@@ -1194,9 +1326,9 @@ int launch_fwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const voi
         auto go = [&](auto sp) {
           constexpr bool SP = decltype(sp)::value;
           if (s.nseg > 1)  // aggregates of every segment but the last
-            hipLaunchKernelGGL((ssm_fwd_kernel<G, false, true, SP, T>), dim3(s.ncb, s.B, s.nseg - 1),
-                               dim3(kWave * G), 0, st, a);
-          hipLaunchKernelGGL((ssm_fwd_kernel<G, E, false, SP, T>), dim3(s.ncb, s.B, s.nseg), dim3(kWave * G), 0,
+            hipLaunchKernelGGL((ssm_fwd_agg_kernel<G, SP, T>), dim3(s.ncb, s.B, s.nseg - 1), dim3(kWave * G), 0,
+                               st, a);
+          hipLaunchKernelGGL((ssm_fwd_kernel<G, E, SP, T>), dim3(s.ncb, s.B, s.nseg), dim3(kWave * G), 0,
                              st, a);
         };
         if (desc->flags & SSM_DELTA_SOFTPLUS) go(std::true_type{}); else go(std::false_type{});
@@ -1232,7 +1364,7 @@ int launch_bwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const voi
   a.ws_dD = ws + wl.dD;
   a.ws_ddt = ws + wl.ddt;
   a.agg_G = ws + wl.aggG;
-  a.agg_S = ws + wl.aggS;
+  a.agg_P = ws + wl.aggP;
   a.Bt = s.B;
   a.L = s.L;
   a.D = s.D;

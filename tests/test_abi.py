@@ -61,7 +61,7 @@ def test_time_split_workspace_follows_the_segment_rule():
     assert fwd_ws(batch=16, seqlen=4096, dim=5120, dstate=16, dtype=L.SSM_BF16) == 0
     # long-sequence shapes split in time: B*ceil(D/32)*ceil(N/4) waves, 2048 slots
     # config 3 (1 x 1M x 1024): 128 waves -> 16 segments; config 2 per direction: 256 -> 8
-    per_seg = lambda B, N, D: B * (N + 1) * D * 4
+    per_seg = lambda B, N, D: B * 2 * N * D * 4  # end state and decay product per (row, state, channel)
     assert fwd_ws(batch=1, seqlen=1 << 20, dim=1024, dstate=16) == 16 * per_seg(1, 16, 1024)
     assert fwd_ws(batch=4, seqlen=131072, dim=512, dstate=16) == 8 * per_seg(4, 16, 512)
     # segments never shorter than 512 steps when chosen automatically

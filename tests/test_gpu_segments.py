@@ -91,7 +91,7 @@ def test_automatic_split_of_a_long_row():
     shape = (1, 16384, 64, 16)
     d = L.make_desc(*shape)
     # 1 x 2 channel blocks x 4 waves: split into 512-step segments
-    assert L.size_query(L.lib().ssm_fwd_workspace_bytes, d) == 32 * 17 * 64 * 4
+    assert L.size_query(L.lib().ssm_fwd_workspace_bytes, d) == 32 * 32 * 64 * 4
     inp = make_inputs(*shape, seed=2)
     y, g = _run(inp)
     yr, gr = _oracle(inp)
@@ -107,6 +107,51 @@ def test_split_and_unsplit_agree():
     _close("y", y2, y1.detach().double().cpu().numpy())
     for k in ("u", "dt", "A", "B", "C", "D", "z"):
         _close(f"d{k}", g2[k], g1[k].double().cpu().numpy())
+
+
+def _tail_log_decay(inp, lo, hi):
+    """log of each (batch, channel, state) decay product over steps [lo, hi): A * sum(delta)."""
+    dsum = inp["dt"][:, lo:hi, :].astype(np.float64).sum(axis=1)  # (B, D)
+    return dsum[:, :, None] * inp["A"].astype(np.float64)[None]
+
+
+@pytest.mark.parametrize("flags", [(), ("reverse", "complement", "skip", "gate")], ids=lambda f: "+".join(f) or "plain")
+def test_aggregate_walks_stop_at_underflow(flags):
+    """Strong decay in long segments: every decay product of segment 0's last
+    1024 steps and of segment 1's first 1024 steps is below exp(-150), so both
+    aggregate walks reach exact zeros part-way through their segment and stop."""
+    inp = make_inputs(1, 4096, 64, 16, seed=21)
+    inp["dt"] = (inp["dt"] * 8.0).astype(np.float32)
+    assert _tail_log_decay(inp, 1024, 2048).max() < -150
+    assert _tail_log_decay(inp, 2048, 3072).max() < -150
+    y, g = _run(inp, flags, segments=2)
+    yr, gr = _oracle(inp, flags)
+    _close("y", y, yr)
+    for k in ("u", "dt", "A", "B", "C"):
+        _close(f"d{k}", g[k], gr[k])
+    if "skip" in flags:
+        _close("dD", g["D"], gr["D"])
+    if "gate" in flags:
+        _close("dz", g["z"], gr["z"])
+
+
+def test_aggregates_without_decay():
+    """States with A = 0 (decay 1 throughout) and A = -1e-6 in some channels keep
+    their workgroup walking the whole segment; the other channel block stops early."""
+    inp = make_inputs(2, 3072, 64, 16, seed=22)
+    inp["dt"] = (inp["dt"] * 8.0).astype(np.float32)
+    inp["A"][3, :] = 0.0
+    inp["A"][5, 7] = 0.0
+    inp["A"][17, 2] = -1e-6
+    assert _tail_log_decay(inp, 0, 1024)[:, 32:].max() < -150  # channels 32..63 decay to 0
+    y, g = _run(inp, ("skip",), segments=3)
+    yr, gr = _oracle(inp, ("skip",))
+    # undecayed states sum thousands of steps (|h| ~ 10), so y and the gradients
+    # carry fp32 rounding at the scale of their largest values
+    at = lambda r: ATOL * max(1.0, float(np.abs(r).max()))
+    _close("y", y, yr, RTOL, at(yr))
+    for k in ("u", "dt", "A", "B", "C", "D"):
+        _close(f"d{k}", g[k], gr[k], RTOL, at(gr[k]))
 
 
 # ------------------------------------------------------------ config 3 shape
@@ -136,7 +181,7 @@ def test_config3_split_is_automatic():
     from selectssm_amd import _lib as L
 
     d = L.make_desc(*SHAPE3)
-    assert L.size_query(L.lib().ssm_fwd_workspace_bytes, d) == 16 * 17 * 1024 * 4
+    assert L.size_query(L.lib().ssm_fwd_workspace_bytes, d) == 16 * 32 * 1024 * 4
 
 
 def test_config3_exact_linearity(inputs3, split3):
