@@ -1170,15 +1170,42 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_agg_k
   }
 }
 
-// out[i] = sum_k ws[k*count + i], k = 0..nparts-1 in order
-template <typename TO>
+// out[i] = sum_k ws[k*count + i], k = 0..nparts-1 in order.  Each thread sums
+// 4 consecutive outputs with 8 parts' loads in flight; V4 (count a multiple of
+// 4, ws 16-byte aligned) loads them as float4.
+template <typename TO, bool V4>
 __global__ void reduce_parts_kernel(const float* __restrict__ ws, TO* __restrict__ out, int nparts,
                                     int64_t count) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= count) return;
-  float s = 0.0f;
-  for (int k = 0; k < nparts; ++k) s += ws[(int64_t)k * count + i];
-  st(out, i, s);
+  const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i0 >= count) return;
+  constexpr int kIn = 8;
+  if constexpr (V4) {
+    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto add = [&](const float4 v) {
+      s[0] += v.x;
+      s[1] += v.y;
+      s[2] += v.z;
+      s[3] += v.w;
+    };
+    int k = 0;
+    for (; k + kIn <= nparts; k += kIn) {
+      float4 v[kIn];
+#pragma unroll
+      for (int j = 0; j < kIn; ++j) v[j] = *reinterpret_cast<const float4*>(ws + (int64_t)(k + j) * count + i0);
+#pragma unroll
+      for (int j = 0; j < kIn; ++j) add(v[j]);
+    }
+    for (; k < nparts; ++k) add(*reinterpret_cast<const float4*>(ws + (int64_t)k * count + i0));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) st(out, i0 + e, s[e]);
+  } else {
+    const int m = (int)(count - i0 < 4 ? count - i0 : 4);
+    for (int e = 0; e < m; ++e) {
+      float sum = 0.0f;
+      for (int k = 0; k < nparts; ++k) sum += ws[(int64_t)k * count + i0 + e];
+      st(out, i0 + e, sum);
+    }
+  }
 }
 
 // ------------------------------------------------------------------- host side
@@ -1390,9 +1417,13 @@ int launch_bwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const voi
   auto reduce = [&](const float* part, auto* out, int nparts, int64_t count) {
     using TO = std::remove_pointer_t<decltype(out)>;
     const int threads = 256;
-    const int64_t blocks = (count + threads - 1) / threads;
-    hipLaunchKernelGGL((reduce_parts_kernel<TO>), dim3((unsigned)blocks), dim3(threads), 0, st, part, out,
-                       nparts, count);
+    const int64_t blocks = ((count + 3) / 4 + threads - 1) / threads;
+    if (count % 4 == 0 && reinterpret_cast<uintptr_t>(part) % 16 == 0)
+      hipLaunchKernelGGL((reduce_parts_kernel<TO, true>), dim3((unsigned)blocks), dim3(threads), 0, st, part,
+                         out, nparts, count);
+    else
+      hipLaunchKernelGGL((reduce_parts_kernel<TO, false>), dim3((unsigned)blocks), dim3(threads), 0, st, part,
+                         out, nparts, count);
   };
   const int64_t bln = (int64_t)s.B * s.L * s.N;
   reduce(ws + wl.dB, static_cast<T*>(dB), s.ncb, bln);
