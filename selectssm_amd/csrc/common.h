@@ -71,6 +71,38 @@ __device__ __forceinline__ void st32(T* base, uint32_t off, float v) {
   st(reinterpret_cast<T*>(reinterpret_cast<char*>(base) + byte), 0, v);
 }
 
+// A tensor base (one batch row) addressed with two 32-bit byte offsets: a
+// per-lane one fixed for the kernel and a wave-uniform one (row arithmetic
+// on scalars).  Their sum is one vector add, and the access is one
+// global_load/store with the base in SGPRs and the sum as its unsigned
+// 32-bit offset, so no per-access 64-bit address math; the host keeps every
+// per-batch-row extent at or below 4 GiB.
+struct buf_t {
+  const char* p;
+};
+__device__ __forceinline__ buf_t make_buf(const void* p) { return buf_t{static_cast<const char*>(p)}; }
+template <typename T>
+__device__ __forceinline__ float bld(buf_t r, uint32_t voff, uint32_t soff) {
+  return ld(reinterpret_cast<const T*>(r.p + (voff + soff)), 0);
+}
+// four consecutive elements (16-byte aligned for f32, 8-byte for bf16)
+template <typename T>
+__device__ __forceinline__ float4 bld4(buf_t r, uint32_t voff, uint32_t soff);
+template <>
+__device__ __forceinline__ float4 bld4<float>(buf_t r, uint32_t voff, uint32_t soff) {
+  return *reinterpret_cast<const float4*>(r.p + (voff + soff));
+}
+template <>
+__device__ __forceinline__ float4 bld4<bf16>(buf_t r, uint32_t voff, uint32_t soff) {
+  const uint2 v = *reinterpret_cast<const uint2*>(r.p + (voff + soff));
+  return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u), __uint_as_float(v.y << 16),
+                     __uint_as_float(v.y & 0xffff0000u));
+}
+template <typename T>
+__device__ __forceinline__ void bst(buf_t r, uint32_t voff, uint32_t soff, float v) {
+  st(reinterpret_cast<T*>(const_cast<char*>(r.p) + (voff + soff)), 0, v);
+}
+
 // Runs f() on the lanes whose channel exists.  A workgroup whose 64 channels
 // all exist (every one when D % 64 == 0) takes a wave-uniform branch and needs
 // no per-lane exec masking.
@@ -125,65 +157,77 @@ __device__ __forceinline__ float softplus(float x) {
 }
 
 // ------------------------------------------------------ cross-lane reductions
+//
+// DPP patterns used below (all within a row of 16 lanes, every lane has a source):
+//   row_ror:8 (0x128)        lane ^ 8
+//   row_half_mirror (0x141)  lane ^ 7 within each group of 8
+//   quad_perm [2,3,0,1]      lane ^ 2
+//   quad_perm [1,0,3,2]      lane ^ 1
 
 template <int CTRL>
-__device__ __forceinline__ float dpp_move(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
 }
+constexpr int kDppRor8 = 0x128;
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppXor2 = 0x4E;
+constexpr int kDppXor1 = 0xB1;
 
-// Sum of v over the 16 lanes of each row; every lane of the row gets it.
-__device__ __forceinline__ float row_sum16(float v) {
-  v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]
-  v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]
-  v += dpp_move<0x141>(v);  // row_half_mirror
-  v += dpp_move<0x140>(v);  // row_mirror
-  return v;
-}
-
-// Sum of v over the 32 lanes of each wave half; every lane of the half gets it.
-__device__ __forceinline__ float half_sum32(float v) {
-  v = row_sum16(v);
-  auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-}
-
-// Lanes l and l^32 hold the two halves of one channel's sum: the result is a
-// summed over the halves in lanes < 32 and b summed over the halves in lanes >= 32.
+// Lanes l and l ^ 32 hold parts of the same sums: the result is a summed over
+// both in lanes < 32 and b summed over both in lanes >= 32.
 __device__ __forceinline__ float half_pair(float a, float b) {
   auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
   return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
 }
 
-// Eight per-lane values, each summed over the 32 lanes of its wave half: 16
-// totals per wave.  Lane l ends with the total of x[reduce32x8_value(l)] over
-// half reduce32x8_half(l); the 4 lanes of each aligned quad hold the same one.
-__device__ __forceinline__ float reduce32x8(const float (&x)[8]) {
-  float p[4];
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {  // rows 0..3 keep x[2m], x[2m+1] of half 0, x[2m], x[2m+1] of half 1
-    auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(x[2 * m]), __float_as_uint(x[2 * m + 1]), false, false);
-    p[m] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-  }
-  const int lid = __lane_id();
-  const bool b3 = (lid & 8) != 0;
-  const bool b2 = (lid & 4) != 0;
-  float q[2];
-#pragma unroll
-  for (int m = 0; m < 2; ++m) {  // lanes with bit 3 clear keep p[2m], set keep p[2m+1]
-    const float keep = b3 ? p[2 * m + 1] : p[2 * m];
-    const float give = b3 ? p[2 * m] : p[2 * m + 1];
-    q[m] = keep + dpp_move<0x128>(give);  // row_ror:8
-  }
-  const float keep = b2 ? q[1] : q[0];    // bit 2 clear keeps q[0], set keeps q[1]
-  const float give = b2 ? q[0] : q[1];
-  float r = keep + dpp_move<0x141>(give);  // row_half_mirror
-  r += dpp_move<0xB1>(r);                  // quad_perm [1,0,3,2]
-  r += dpp_move<0x4E>(r);                  // quad_perm [2,3,0,1]
-  return r;
+// Rows r and r ^ 1 (16 lanes each) hold parts of the same sums: rows 0 and 2
+// get a summed over their row pair, rows 1 and 3 get b summed over theirs.
+__device__ __forceinline__ float row_pair(float a, float b) {
+  auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
 }
-__device__ __forceinline__ int reduce32x8_value(int lane) {
-  return 4 * ((lane >> 2) & 1) + 2 * ((lane >> 3) & 1) + ((lane >> 4) & 1);
+
+// Four per-lane values (consecutive steps 0..3), each summed over the 4 rows
+// of the wave: row r ends with step yrow_step(r) (rows hold 0, 2, 1, 3).
+__device__ __forceinline__ float rows_transpose_sum4(float y0, float y1, float y2, float y3) {
+  return row_pair(half_pair(y0, y1), half_pair(y2, y3));
 }
-__device__ __forceinline__ int reduce32x8_half(int lane) { return lane >> 5; }
+__device__ __forceinline__ int yrow_step(int row) { return ((row & 1) << 1) | (row >> 1); }
+
+// Sum over the 8 lanes c = lane & 7 of each half-row, of S per-lane values
+// whose state order is permuted by the lane: x[j] holds state j ^ sig with
+// sig = chan_sig<S>(c).  Pairing lanes whose sig differ lets one DPP add
+// combine two states (each lane keeps the state its partner sends), so the S
+// values cost S - 1 adds before the remaining channel bits are summed plainly.
+// The result in lane c is state chan_sig<S>(c) summed over the 8 channels.
+//   S = 2: sig = c2.  lane ^ 7 flips sig: x0 + x1'; then plain lane ^ 2, ^ 1.
+//   S = 4: sig = (c0 ^ c1 ^ c2) | c2 << 1.  lane ^ 7 flips both bits of sig:
+//          x0 + x3', x1 + x2'; lane ^ 1 flips bit 0: r0 + r1'; then plain
+//          lane ^ 3, which keeps sig.  The pairings ^7, ^1, ^3 reach all 8.
+template <int S>
+__device__ __forceinline__ int chan_sig(int c) {
+  if constexpr (S == 1) return 0;
+  else if constexpr (S == 2) return (c >> 2) & 1;
+  else return ((c ^ (c >> 1) ^ (c >> 2)) & 1) | (((c >> 2) & 1) << 1);
+}
+constexpr int kDppXor3 = 0x1B;  // quad_perm [3,2,1,0]: lane ^ 3
+template <int S>
+__device__ __forceinline__ float chan_reduce8(const float (&x)[S]) {
+  static_assert(S == 1 || S == 2 || S == 4, "1, 2 or 4 states per lane");
+  if constexpr (S == 1) {
+    float r = x[0] + dpp_mov<kDppHalfMirror>(x[0]);
+    r += dpp_mov<kDppXor2>(r);
+    return r + dpp_mov<kDppXor1>(r);
+  } else if constexpr (S == 2) {
+    float r = x[0] + dpp_mov<kDppHalfMirror>(x[1]);
+    r += dpp_mov<kDppXor2>(r);
+    return r + dpp_mov<kDppXor1>(r);
+  } else {
+    const float r0 = x[0] + dpp_mov<kDppHalfMirror>(x[3]);
+    const float r1 = x[1] + dpp_mov<kDppHalfMirror>(x[2]);
+    const float r = r0 + dpp_mov<kDppXor1>(r1);
+    return r + dpp_mov<kDppXor3>(r);
+  }
+}
 
 }  // namespace ssm

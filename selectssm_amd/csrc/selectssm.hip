@@ -1,37 +1,45 @@
 // selectssm.hip — selective-scan forward/backward for MI355X (gfx950, CDNA4).
 //
-// Work decomposition (both kernels)
-//   * workgroup = (block of 32 channels, batch row, time segment); time runs
-//     sequentially inside the workgroup.  With 32 channels per workgroup a CU
-//     holds two workgroups whose barriers are independent.
-//   * rows too few to fill the chip (B * ceil(D/32) small: long-sequence
-//     shapes) are split in time into segments joined by carries: an aggregate
-//     pass gives each segment's (decay product P, end state H from a zero
-//     start), and each segment of the main pass folds the earlier segments'
-//     aggregates into its starting state, h = P h + H (the combine of
-//     selectssm.py:81-85 applied to whole segments).  The backward does the
-//     same for the adjoint carry, right to left.  The aggregate walks flush
-//     products below 2^-126 to zero and stop where every P of the workgroup
-//     is 0, since all further terms are then exact zeros.
-//   * lane = channel: lane l holds channel l & 31, and the two 32-lane halves
-//     of a wave hold different states of the same 32 channels.  Each lane keeps
-//     2 states, a wave 4, and the NG = ceil(N/4) waves of a workgroup all N.
-//     u / delta / dy / y rows ((B,L,D) row-major) move as 128-byte rows; the
-//     sum over states (y, du, ddelta) is one cross-half add plus an LDS sum
-//     over the NG waves.
-//   * A[d,n] lives in VGPRs pre-scaled by log2(e), so the decay is one
-//     v_exp_f32 of one product; B_t,n / C_t,n are read from LDS as broadcasts.
-//   * time is walked in tiles staged in LDS: the next tile's loads are issued
-//     before the current tile computes and written to the other buffer after.
+// Both kernels give each workgroup 64 channels of one batch row and one time
+// segment; time runs sequentially inside the workgroup, and all states of a
+// channel live in one wave, so every sum over states stays inside the wave.
 //
-// Backward = the custom-VJP adjoint of ssmrecscan.py:150-160 with the
-// recursive storage of ssmrecscan.py:111-148 replaced by checkpoints: the
-// forward stores h entering every 16-step block; the backward walks blocks in
-// reverse, recomputes a_t and h_{t-1} of the block into registers, then runs
-// the adjoint f_t = C_t dy_t + a_{t+1} f_{t+1} backwards through the block.
-// Sums over channels (dB, dC) are reduced within each 32-lane half with
-// v_permlane16_swap + DPP, 4 steps at a time, then across channel blocks in
-// fixed order, so every gradient is deterministic.
+// Forward (ssm_fwd_kernel): 4 waves.  lane = c + 16 g holds channel c of the
+// wave's 16 and the SPL states SPL*g .. SPL*g + SPL - 1 (state row g), so a
+// lane carries SPL = 4 states for N <= 16.  Per step and state: one v_exp_f32
+// of A*log2(e)*delta, h = a h + B (delta u), y += C h.  The sum over the 4
+// state rows of 4 consecutive steps is one transposed exchange (2 x
+// v_permlane32_swap + v_permlane16_swap and 3 adds): row r ends with step
+// yrow_step(r), and every lane stores one (step, channel) of y.
+//
+// Backward (ssm_bwd_kernel): 8 waves.  lane = c + 8 g holds channel c of the
+// wave's 8 and SPL states of state group g (SPL = 2 for N <= 16), in an order
+// permuted by the lane (state SPL*g + (j ^ sig(c)) in slot j) so that the sums
+// over channels for dB and dC take one DPP add per pair of states
+// (chan_reduce8).  The sums over states (du, ddelta) of 2 steps are one
+// transposed exchange over the 8 groups.  The custom-VJP adjoint of
+// ssmrecscan.py:150-160 with the recursive storage of ssmrecscan.py:111-148
+// replaced by checkpoints: the forward stores h entering every block of 16
+// steps; the backward walks blocks in reverse, recomputes a_t and h_{t-1} of
+// the block into registers, then runs the adjoint f_t = C_t dy_t + a_{t+1}
+// f_{t+1} backwards through the block.
+//
+// Rows too few to fill the chip (long-sequence shapes) are split in time into
+// segments joined by carries: an aggregate pass gives each segment's (decay
+// product P, end state H from a zero start), and each segment of the main pass
+// folds the earlier segments' aggregates into its starting state, h = P h + H
+// (the combine of selectssm.py:81-85 applied to whole segments); the backward
+// does the same for the adjoint carry, right to left.  The aggregate walks
+// flush products below 2^-126 to zero and stop where every P of the workgroup
+// is 0, since all further terms are then exact zeros.
+//
+// Time is walked in tiles staged in LDS: the next tile's global loads are
+// issued before the current tile computes and written to the other buffer
+// after it; inside a tile the LDS operands of step i + PF are read while step
+// i computes (sched_barrier keeps the reads where they are written).  Sums
+// over channel blocks (dB, dC, broadcast ddelta) and over rows / segments
+// (dA, dD) go through partial buffers reduced in a fixed order, so every
+// gradient is deterministic.
 
 #include <hip/hip_runtime.h>
 
@@ -49,26 +57,51 @@ namespace {
 using namespace ssm;
 
 constexpr int kWave = 64;
-constexpr int kCh = 32;   // channels per workgroup (lane & 31)
-constexpr int kSPW = 4;   // states per wave: 2 per lane, the two lane halves differ
-constexpr int kTT = 32;   // forward time tile
-constexpr int kCK = 16;   // checkpoint interval = backward block length
-#ifndef SSM_BWD_RB
-#define SSM_BWD_RB 16
-#endif
-#ifndef SSM_BWD_PF
-#define SSM_BWD_PF 2
-#endif
+constexpr int kBlkCh = 64;    // channels per workgroup
+constexpr int kFwdWaves = 4;  // forward: 16 channels x 4 state rows per wave
+constexpr int kBwdWaves = 8;  // backward: 8 channels x 8 state groups per wave
+constexpr int kTT = 32;       // forward time tile
+constexpr int kCK = 16;       // checkpoint interval = backward block length
 #ifndef SSM_FWD_PF
 #define SSM_FWD_PF 2
 #endif
-#ifndef SSM_LDS_DB
-#define SSM_LDS_DB 1
+#ifndef SSM_BWD_PF
+#define SSM_BWD_PF 1
 #endif
-#ifndef SSM_LDS_DC
-#define SSM_LDS_DC 0
-#endif
-constexpr int kRS = 36;   // padded row (floats) of the dB / dC transpose tile: 16-lane float4 reads hit distinct banks
+
+// S consecutive floats of LDS (16-byte aligned when S >= 4) into registers
+template <int S>
+__device__ __forceinline__ void lds_vec(const float* p, float (&v)[S]) {
+  if constexpr (S == 1) {
+    v[0] = p[0];
+  } else if constexpr (S == 2) {
+    const float2 t = *reinterpret_cast<const float2*>(p);
+    v[0] = t.x;
+    v[1] = t.y;
+  } else {
+    static_assert(S % 4 == 0, "vector of 1, 2 or a multiple of 4 floats");
+#pragma unroll
+    for (int k = 0; k < S / 4; ++k) {
+      const float4 t = reinterpret_cast<const float4*>(p)[k];
+      v[4 * k] = t.x;
+      v[4 * k + 1] = t.y;
+      v[4 * k + 2] = t.z;
+      v[4 * k + 3] = t.w;
+    }
+  }
+}
+
+// A segment's running decay product is flushed to zero once it falls below
+// the smallest normal float (2^-126), as in flush-to-zero arithmetic: with
+// subnormals kept, a product whose step factors exceed 1/2 stalls at the
+// smallest subnormal instead of reaching 0.  What the flush drops is below
+// 2^-126 times the later terms; it would matter only if the remaining decays
+// grew by some 2^100 within the segment, which A <= 0, delta >= 0 rule out.
+template <int S>
+__device__ __forceinline__ void flush_tiny(float (&P)[S]) {
+#pragma unroll
+  for (int j = 0; j < S; ++j) P[j] = P[j] < 0x1p-126f ? 0.0f : P[j];
+}
 
 // --------------------------------------------------------------- forward
 
@@ -92,39 +125,47 @@ struct FwdArgs {
   uint32_t flags;
 };
 
-// NG waves (4 states each) per workgroup; EPI: the extra staging of the
-// reverse skip and the gate.  Workgroup (cb, b, seg) scans time segment seg of
-// its rows, starting from the state the earlier segments hand over (folded
-// from their aggregates, ssm_fwd_agg_kernel), and writes y and the
-// checkpoints.
-// SP: delta arrives before softplus (SSM_DELTA_SOFTPLUS); a separate build,
-// because carrying the unused softplus code in the time loop slows it down.
-template <int NG, bool EPI, bool SP, typename T>
-__global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kernel(FwdArgs<T> p) {
-  constexpr int NS = NG * kSPW;         // padded state count
-  constexpr int NT = kWave * NG;        // threads
-  constexpr int RPT = kTT * kCh / NT;   // staged (step, channel) elements per thread
-  constexpr int RSTEP = NT / kCh;       // staged rows between a thread's elements
-  constexpr int BCE = kTT * NS / NT;    // staged B / C elements per thread
-  static_assert(BCE * NT == kTT * NS && RPT * NT == kTT * kCh, "staging must tile exactly");
-  static_assert(kTT % kCK == 0, "time tile must hold whole checkpoint blocks");
+// Staging of a forward tile (kTT steps x 64 channels) by the 256 threads:
+// thread -> column scol (channel cb*64 + scol), rows srow0 + k*4, k < 8.  A
+// wave loads whole 64-channel rows, so each load instruction is 256
+// contiguous bytes (fp32).
+struct FwdStage {
+  static constexpr int NT = kWave * kFwdWaves;
+  static constexpr int RPT = kTT * kBlkCh / NT;
+  static constexpr int RSTEP = NT / kBlkCh;
+};
+
+// Workgroup (cb, b, seg) scans time segment seg of its 64 channels, starting
+// from the state the earlier segments hand over (folded from their
+// aggregates, ssm_fwd_agg_kernel), and writes y and the checkpoints.
+// SPL: states per lane (N <= 4 * SPL).  EPI: the extra staging of the reverse
+// skip and the gate.  SP: delta arrives before softplus (SSM_DELTA_SOFTPLUS).
+// VEC: u and delta rows are read as aligned 4-element vectors (D % 4 == 0,
+// per-channel delta); chosen per launch, so every tile stages the same way.
+template <int SPL, bool EPI, bool SP, bool VEC, typename T>
+__global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T> p) {
+  constexpr int NS = 4 * SPL;  // padded state count
+  constexpr int NT = FwdStage::NT, RPT = FwdStage::RPT, RSTEP = FwdStage::RSTEP;
+  constexpr int BCN = kTT * NS;                 // staged B (or C) elements per tile
+  constexpr int BCE = (BCN + NT - 1) / NT;      // per thread
   constexpr int EB = EPI ? 2 : 1;
   constexpr int ER = EPI ? kTT : 1;
+  constexpr int PF = SSM_FWD_PF;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int c = lane & (kCh - 1);
-  const int hf = lane >> 5;
+  const int c = lane & 15;
+  const int g = lane >> 4;
   const int b = blockIdx.y;
   const int cb = blockIdx.x;
   const int seg = blockIdx.z;
   const int L = p.L, D = p.D, N = p.N;
   const int t_lo = seg * p.seg_len;
   const int t_hi = min(L, t_lo + p.seg_len);
-  const int d = cb * kCh + c;
+  const int cw = wave * 16 + c;  // channel within the block
+  const int d = cb * kBlkCh + cw;
   const bool valid = d < D;
   const int dc = valid ? d : 0;
-  const int n0 = wave * kSPW + 2 * hf;  // this lane's states n0, n0 + 1
   const bool rev = p.flags & SSM_REVERSE;
   const bool comp = rev && (p.flags & SSM_COMPLEMENT);
   // the skip of a forward scan uses the staged u itself; the reverse skip and
@@ -132,114 +173,160 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kerne
   const bool skip = (p.flags & SSM_SKIP) != 0;
   const bool gate = EPI && (p.flags & SSM_GATE);
   const bool stage_eu = EPI && skip && rev;  // u at the output position is another element
-  // staging / output mapping: thread -> column scol, rows srow0 + k * RSTEP
-  const int scol = tid & (kCh - 1);
-  const int srow0 = tid / kCh;
-  const int sd = cb * kCh + scol;
+  const int q = comp ? D - 1 - dc : dc;      // output channel of this lane
+  const float Dq = (skip && valid) ? p.Dskip[q] : 0.0f;
+  const int scol = tid & (kBlkCh - 1);
+  const int srow0 = wave;  // = tid / kBlkCh: the staged rows of a wave are uniform
+  const int sd = cb * kBlkCh + scol;
   const bool svalid = sd < D;
-  const bool full_cb = (cb + 1) * kCh <= D;
   const int sdc = svalid ? sd : 0;
   const int sq = comp ? D - 1 - sdc : sdc;  // output channel of the staged column
-  const float Dq = (skip && svalid) ? p.Dskip[sq] : 0.0f;
+  const bool full_cb = (cb + 1) * kBlkCh <= D;
 
-  float A2[2], h[2];
+  float A2[SPL], h[SPL];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int n = n0 + j;
-    A2[j] = (valid && n < N) ? p.A[(int64_t)dc * N + n] * kLog2e : 0.0f;
+  for (int j = 0; j < SPL; ++j) {
+    const int n = SPL * g + j;
+    A2[j] = (valid && n < N) ? p.A[dc * N + n] * kLog2e : 0.0f;
     h[j] = 0.0f;
   }
   if (seg > 0) {
     // state entering this segment: h = P h + H over the earlier segments in
     // order (the combine of selectssm.py:81-85 applied to whole segments)
     const int64_t base = (int64_t)b * p.nseg * N * D + dc;
-    const int nc0 = min(n0, N - 1), nc1 = min(n0 + 1, N - 1);
-#pragma unroll 4
+#pragma unroll 2
     for (int s = 0; s < seg; ++s) {
-      const int64_t o0 = base + ((int64_t)s * N + nc0) * D, o1 = base + ((int64_t)s * N + nc1) * D;
-      h[0] = fmaf(p.agg_P[o0], h[0], p.agg_H[o0]);
-      h[1] = fmaf(p.agg_P[o1], h[1], p.agg_H[o1]);
+#pragma unroll
+      for (int j = 0; j < SPL; ++j) {
+        const int64_t o = base + ((int64_t)s * N + min(SPL * g + j, N - 1)) * D;
+        h[j] = fmaf(p.agg_P[o], h[j], p.agg_H[o]);
+      }
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      if (!(valid && n0 + j < N)) h[j] = 0.0f;
+    for (int j = 0; j < SPL; ++j)
+      if (!(valid && SPL * g + j < N)) h[j] = 0.0f;
   }
 
-  __shared__ float s_u[2][kTT][kCh], s_dt[2][kTT][kCh];
-  __shared__ float s_eu[EB][ER][kCh], s_ez[EB][ER][kCh];
+  __shared__ float2 s_ud[2][kTT][kBlkCh];  // (u, delta)
+  __shared__ float s_eu[EB][ER][kBlkCh], s_ez[EB][ER][kBlkCh];
   __shared__ __attribute__((aligned(16))) float s_B[2][kTT][NS];
   __shared__ __attribute__((aligned(16))) float s_C[2][kTT][NS];
-  __shared__ float s_y[NG][kTT][kCh];
 
-  const int64_t bLD = (int64_t)b * L * D;
-  const int64_t bLN = (int64_t)b * L * N;
   const int dtD = p.dstride ? D : 1;
-  const int64_t bLDt = (int64_t)b * L * dtD;
   const int scol_dt = p.dstride ? sdc : 0;
-  const T* __restrict__ u_b = p.u + bLD;
-  const T* __restrict__ dt_b = p.delta + bLDt;
+  const T* __restrict__ u_b = p.u + (int64_t)b * L * D;
+  const T* __restrict__ dt_b = p.delta + (int64_t)b * L * dtD;
   const int ldy = p.ldy, ldz = p.ldz;
   const T* __restrict__ z_b = EPI ? p.z + (int64_t)b * L * ldz : nullptr;
-  const T* __restrict__ B_b = p.Bc + bLN;
-  const T* __restrict__ C_b = p.Cc + bLN;
+  const T* __restrict__ B_b = p.Bc + (int64_t)b * L * N;
+  const T* __restrict__ C_b = p.Cc + (int64_t)b * L * N;
   T* __restrict__ y_b = p.y + (int64_t)b * L * ldy;
   float* __restrict__ ck_b = p.ckpt != nullptr ? p.ckpt + (int64_t)b * p.nblk * N * D : nullptr;
   const int LN = L * N;
   const int ND = N * D;
+  const buf_t ru = make_buf(u_b), rdt = make_buf(dt_b), rB = make_buf(B_b), rC = make_buf(C_b);
+  const buf_t rz = make_buf(EPI ? z_b : u_b), ry = make_buf(y_b), rck = make_buf(ck_b != nullptr ? ck_b : p.A);
+  const uint32_t cb_c = (uint32_t)(sdc * sizeof(T)), cb_q = (uint32_t)(sq * sizeof(T));
+  const uint32_t cb_dt = (uint32_t)(scol_dt * sizeof(T));
 
   // fetch() only issues loads (clamped addresses, raw values); commit(), run
   // after the tile's compute, zeroes what lies outside the tensor and writes
-  // LDS, so the loads' latency is covered by a whole tile.
+  // LDS, so the loads' latency is covered by a whole tile.  VEC launches read
+  // u and delta as 4-element vectors: thread -> rows vr, vr + 16, channels
+  // vc .. vc + 3 (D % 4 == 0, so a vector is wholly inside or outside D).
   float r_u[RPT], r_dt[RPT], r_eu[RPT], r_ez[RPT], r_B[BCE], r_C[BCE];
+  float4 v_u[2], v_dt[2];
+  static_assert(RPT == 8 && NT == 256, "vector staging covers 2 rows of 4 channels per thread");
+  const int vr = tid >> 4, vc = (tid & 15) * 4;
+  const bool vin = cb * kBlkCh + vc < D;
+  const uint32_t vcb = (uint32_t)((vin ? cb * kBlkCh + vc : 0) * sizeof(T));
+  const uint32_t rowb = (uint32_t)(D * sizeof(T));  // bytes per (B,L,D) row
   auto fetch = [&](int t0) {
+    if constexpr (VEC) {
 #pragma unroll
-    for (int k = 0; k < RPT; ++k) {
-      const int tc = min(t0 + srow0 + k * RSTEP, L - 1);
-      r_u[k] = ld32(u_b, (uint32_t)(tc * D + sdc));
-      r_dt[k] = ld32(dt_b, (uint32_t)(tc * dtD + scol_dt));
-      if (stage_eu || gate) {
-        const int pr = rev ? L - 1 - tc : tc;
-        if (stage_eu) r_eu[k] = ld32(u_b, (uint32_t)(pr * D + sq));
-        if (gate) r_ez[k] = ld32(z_b, (uint32_t)(pr * ldz + sq));
+      for (int k = 0; k < 2; ++k) {
+        const uint32_t o = (uint32_t)min(t0 + vr + 16 * k, L - 1) * rowb + vcb;
+        v_u[k] = bld4<T>(ru, o, 0);
+        v_dt[k] = bld4<T>(rdt, o, 0);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < RPT; ++k) {
+        const int tc = min(t0 + srow0 + k * RSTEP, L - 1);  // wave-uniform
+        r_u[k] = bld<T>(ru, cb_c, (uint32_t)tc * rowb);
+        r_dt[k] = bld<T>(rdt, cb_dt, (uint32_t)(tc * dtD * sizeof(T)));
       }
     }
 #pragma unroll
     for (int k = 0; k < BCE; ++k) {
       const int e = tid + k * NT;
-      int gi;
-      if (NS == N) {
-        gi = t0 * N + e;
-      } else {
-        const int i = e / NS, n = e - i * NS;
-        gi = (t0 + i) * N + min(n, N - 1);
+      if (BCN % NT == 0 || e < BCN) {
+        const int i = e / NS, n = e - (e / NS) * NS;
+        const uint32_t o = (uint32_t)(min((t0 + i) * N + min(n, N - 1), LN - 1) * sizeof(T));
+        r_B[k] = bld<T>(rB, o, 0);
+        r_C[k] = bld<T>(rC, o, 0);
       }
-      const int gc = min(gi, LN - 1);
-      r_B[k] = ld32(B_b, (uint32_t)gc);
-      r_C[k] = ld32(C_b, (uint32_t)gc);
+    }
+    if (stage_eu || gate) {
+#pragma unroll
+      for (int k = 0; k < RPT; ++k) {
+        const int tc = min(t0 + srow0 + k * RSTEP, L - 1);
+        const int pr = rev ? L - 1 - tc : tc;
+        if (stage_eu) r_eu[k] = bld<T>(ru, cb_q, (uint32_t)pr * rowb);
+        if (gate) r_ez[k] = bld<T>(rz, cb_q, (uint32_t)(pr * ldz * sizeof(T)));
+      }
     }
   };
   auto commit = [&](int buf, int t0) {
+    if constexpr (VEC) {
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const bool in = vin && t0 + vr + 16 * k < L;
+        const float4 uv = v_u[k], dr = v_dt[k];
+        const float4 dv = SP ? make_float4(softplus(dr.x), softplus(dr.y), softplus(dr.z), softplus(dr.w)) : dr;
+        float4* dst = reinterpret_cast<float4*>(&s_ud[buf][vr + 16 * k][vc]);
+        dst[0] = in ? make_float4(uv.x, dv.x, uv.y, dv.y) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        dst[1] = in ? make_float4(uv.z, dv.z, uv.w, dv.w) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < RPT; ++k) {
+        const int i = srow0 + k * RSTEP;
+        const bool in = svalid && t0 + i < L;
+        s_ud[buf][i][scol] = in ? make_float2(r_u[k], SP ? softplus(r_dt[k]) : r_dt[k]) : make_float2(0.0f, 0.0f);
+      }
+    }
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
       const int i = srow0 + k * RSTEP;
       const bool in = svalid && t0 + i < L;
-      s_dt[buf][i][scol] = in ? (SP ? softplus(r_dt[k]) : r_dt[k]) : 0.0f;
-      s_u[buf][i][scol] = in ? r_u[k] : 0.0f;
       if (stage_eu) s_eu[buf][i][scol] = in ? r_eu[k] : 0.0f;
       if (gate) s_ez[buf][i][scol] = in ? r_ez[k] : 0.0f;
     }
 #pragma unroll
     for (int k = 0; k < BCE; ++k) {
       const int e = tid + k * NT;
-      const int i = e / NS, n = e - (e / NS) * NS;
-      const bool in = t0 + i < L && n < N;
-      (&s_B[buf][0][0])[e] = in ? r_B[k] : 0.0f;
-      (&s_C[buf][0][0])[e] = in ? r_C[k] : 0.0f;
+      if (BCN % NT == 0 || e < BCN) {
+        const int i = e / NS, n = e - (e / NS) * NS;
+        const bool in = t0 + i < L && n < N;
+        (&s_B[buf][0][0])[e] = in ? r_B[k] : 0.0f;
+        (&s_C[buf][0][0])[e] = in ? r_C[k] : 0.0f;
+      }
     }
   };
 
+  const int yoff = yrow_step(g);  // step of each 4-step group this lane's row ends with
+  // y of step t0 + i - 3 + yoff is stored at row t0 + i - 3 + yoff, or with
+  // the reverse map at L-1-(t0+i) + (3 - yoff): a uniform row plus this offset
+  const uint32_t yo = (uint32_t)(((rev ? 3 - yoff : yoff) * ldy + q) * sizeof(T));
+  const uint32_t yrowb = (uint32_t)(ldy * sizeof(T));
+  uint32_t cko[SPL];  // checkpoint offsets of this lane's states within a block
+#pragma unroll
+  for (int j = 0; j < SPL; ++j) cko[j] = (uint32_t)(((SPL * g + j) * D + d) * sizeof(float));
+  const uint32_t ckrowb = (uint32_t)(ND * sizeof(float));  // bytes per checkpoint block
   // segments start on tile boundaries (seg_len is a multiple of kTT), so
-  // only the tile at L can be partial
+  // only the tile at L can be partial; its steps beyond L are zeros, which
+  // leave h unchanged, and are not stored
   fetch(t_lo);
   commit(0, t_lo);
   __syncthreads();
@@ -247,103 +334,80 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_kerne
   for (int t0 = t_lo; t0 < t_hi; t0 += kTT, buf ^= 1) {
     const bool more = t0 + kTT < t_hi;
     if (more) fetch(t0 + kTT);
-    const int tn = min(kTT, L - t0);
-    auto tile = [&](auto full_tag) {
+    // a full tile (every channel and state exists, no step beyond L) runs
+    // without per-lane predicates; tiles of a launch without checkpoints
+    // (inference) skip their stores
+    const bool full = full_cb && N == NS && t0 + kTT <= L;
+    auto tile = [&](auto full_tag, auto ck_tag) {
       constexpr bool kFull = decltype(full_tag)::value;
-      // operands of the whole tile in registers first, so no step waits on LDS
-      float uu[kTT], dd[kTT], ys[kTT];
+      constexpr bool kCkpt = decltype(ck_tag)::value;
+      // operands of steps i .. i + PF in a ring of PF + 1 register sets
+      constexpr int R = PF + 1;
+      float2 ud[R];
+      float Bq[R][SPL], Cq[R][SPL];
+      auto pre = [&](int i) {
+        ud[i % R] = s_ud[buf][i][cw];
+        lds_vec<SPL>(&s_B[buf][i][SPL * g], Bq[i % R]);
+        lds_vec<SPL>(&s_C[buf][i][SPL * g], Cq[i % R]);
+      };
+#pragma unroll
+      for (int i = 0; i < PF; ++i) pre(i);
+      float yp[4];
 #pragma unroll
       for (int i = 0; i < kTT; ++i) {
-        if (kFull || i < tn) {
-          uu[i] = s_u[buf][i][c];
-          dd[i] = s_dt[buf][i][c];
-        }
-      }
-      {
-        // B_t, C_t read FPF steps ahead of use, before the y writes in between
-        constexpr int FPF = SSM_FWD_PF;
-        float2 Bl[kTT], Cl[kTT];
+        if (i + PF < kTT) pre(i + PF);
+        __builtin_amdgcn_sched_barrier(0);
+        if (kCkpt && (i % kCK) == 0 && (kFull || t0 + i < L)) {
+          const uint32_t ro = (uint32_t)((t0 + i) / kCK) * ckrowb;
 #pragma unroll
-        for (int i = 0; i < FPF; ++i) {
-          Bl[i] = *reinterpret_cast<const float2*>(&s_B[buf][i][n0]);
-          Cl[i] = *reinterpret_cast<const float2*>(&s_C[buf][i][n0]);
-        }
-#pragma unroll
-        for (int i = 0; i < kTT; ++i) {
-          if (FPF > 0 && i + FPF < kTT) {
-            Bl[i + FPF] = *reinterpret_cast<const float2*>(&s_B[buf][i + FPF][n0]);
-            Cl[i + FPF] = *reinterpret_cast<const float2*>(&s_C[buf][i + FPF][n0]);
-          }
-          ys[i] = 0.0f;
-          if (kFull || i < tn) {
-            const float2 Bv = FPF > 0 ? Bl[i] : *reinterpret_cast<const float2*>(&s_B[buf][i][n0]);
-            const float2 Cv = FPF > 0 ? Cl[i] : *reinterpret_cast<const float2*>(&s_C[buf][i][n0]);
-            if (ck_b != nullptr && (i % kCK) == 0) {
-              const int blk = (t0 + i) / kCK;
-#pragma unroll
-              for (int j = 0; j < 2; ++j)
-                if (valid && n0 + j < N) st32(ck_b, (uint32_t)(blk * ND + (n0 + j) * D + d), h[j]);
-            }
-            const float w = dd[i] * uu[i];
-            const float a0 = fast_exp2(A2[0] * dd[i]);
-            const float a1 = fast_exp2(A2[1] * dd[i]);
-            h[0] = fmaf(a0, h[0], Bv.x * w);
-            h[1] = fmaf(a1, h[1], Bv.y * w);
-            ys[i] = fmaf(Cv.y, h[1], Cv.x * h[0]);
+          for (int j = 0; j < SPL; ++j) {
+            const int n = SPL * g + j;
+            if (kFull || (valid && n < N)) bst<float>(rck, cko[j], ro, h[j]);
           }
         }
-        // add the two halves of each step's sum: even steps land in lanes < 32,
-        // odd steps in lanes >= 32
+        const float uu = ud[i % R].x, dd = ud[i % R].y;
+        const float w = dd * uu;
+        float ys = 0.0f;
 #pragma unroll
-        for (int i = 0; i < kTT; i += 2)
-          if (kFull || i < tn) s_y[wave][i + hf][c] = half_pair(ys[i], ys[i + 1]);
+        for (int j = 0; j < SPL; ++j) {
+          const float a = fast_exp2(A2[j] * dd);
+          h[j] = fmaf(a, h[j], Bq[i % R][j] * w);
+          ys = j == 0 ? Cq[i % R][0] * h[0] : fmaf(Cq[i % R][j], h[j], ys);
+        }
+        yp[i & 3] = ys;
+        if ((i & 3) == 3) {
+          // y of steps i-3..i summed over the state rows: this lane's row holds step ti
+          float yv = rows_transpose_sum4(yp[0], yp[1], yp[2], yp[3]);
+          const int ti = i - 3 + yoff;
+          const int t = t0 + ti;
+          // skip (Dq is 0 without it): u at the output position, which the
+          // reverse map makes another element (staged in EPI builds)
+          float uo = s_ud[buf][ti][cw].x;
+          if constexpr (EPI) {
+            if (stage_eu) uo = s_eu[buf][ti][cw];
+          }
+          yv = fmaf(uo, Dq, yv);
+          if (gate) {
+            const float zz = s_ez[buf][ti][cw];
+            yv *= zz * sigmoid(zz);
+          }
+          if constexpr (kFull) {
+            // the uniform row L-1-(t0+i) is >= 0 on a full tile
+            bst<T>(ry, yo, (uint32_t)(rev ? L - 1 - t0 - i : t0 + i - 3) * yrowb, yv);
+          } else if (valid && t < L) {
+            bst<T>(ry, (uint32_t)(rev ? L - 1 - t : t) * yrowb + (uint32_t)(q * sizeof(T)), 0, yv);
+          }
+        }
       }
     };
-    if (tn == kTT) tile(std::true_type{}); else tile(std::false_type{});
-    {
-      __syncthreads();
-      auto yreduce = [&](auto full_tag) {
-        constexpr bool kFull = decltype(full_tag)::value;
-#pragma unroll
-        for (int k = 0; k < RPT; ++k) {
-          const int i = srow0 + k * RSTEP;
-          if (kFull || i < tn) {
-            float ys = 0.0f;
-#pragma unroll
-            for (int w = 0; w < NG; ++w) ys += s_y[w][i][scol];
-            const int t = t0 + i;
-            const int pt = rev ? L - 1 - t : t;
-            if (skip) {
-              float uo = s_u[buf][i][scol];
-              if constexpr (EPI) {
-                if (stage_eu) uo = s_eu[buf][i][scol];
-              }
-              ys = fmaf(uo, Dq, ys);
-            }
-            if (gate) {
-              const float zz = s_ez[buf][i][scol];
-              ys *= zz * sigmoid(zz);
-            }
-            on_valid_lanes(full_cb, svalid, [&] { st32(y_b, (uint32_t)(pt * ldy + sq), ys); });
-          }
-        }
-      };
-      if (tn == kTT) yreduce(std::true_type{}); else yreduce(std::false_type{});
+    if (ck_b != nullptr) {
+      if (full) tile(std::true_type{}, std::true_type{}); else tile(std::false_type{}, std::true_type{});
+    } else {
+      if (full) tile(std::true_type{}, std::false_type{}); else tile(std::false_type{}, std::false_type{});
     }
     if (more) commit(buf ^ 1, t0 + kTT);
     __syncthreads();
   }
-}
-
-// A segment's running decay product is flushed to zero once it falls below
-// the smallest normal float (2^-126), as in flush-to-zero arithmetic: with
-// subnormals kept, a product whose step factors exceed 1/2 stalls at the
-// smallest subnormal instead of reaching 0.  What the flush drops is below
-// 2^-126 times the later terms; it would matter only if the remaining decays
-// grew by some 2^100 within the segment, which A <= 0, delta >= 0 rule out.
-__device__ __forceinline__ void flush_tiny(float (&P)[2]) {
-#pragma unroll
-  for (int j = 0; j < 2; ++j) P[j] = P[j] < 0x1p-126f ? 0.0f : P[j];
 }
 
 // Forward aggregate pass of a time-split scan.  Workgroup (cb, b, seg), for
@@ -354,46 +418,47 @@ __device__ __forceinline__ void flush_tiny(float (&P)[2]) {
 // workgroup is 0 (flushed at tile ends, flush_tiny) all earlier steps add
 // exact zeros and the walk stops there: with decaying states only the last
 // few thousand steps of a long segment are read.
-template <int NG, bool SP, typename T>
-__global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_agg_kernel(FwdArgs<T> p) {
-  constexpr int NS = NG * kSPW;
-  constexpr int NT = kWave * NG;
-  constexpr int RPT = kTT * kCh / NT;
-  constexpr int RSTEP = NT / kCh;
-  constexpr int BCE = kTT * NS / NT;
-  static_assert(BCE * NT == kTT * NS && RPT * NT == kTT * kCh, "staging must tile exactly");
+template <int SPL, bool SP, typename T>
+__global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_agg_kernel(FwdArgs<T> p) {
+  constexpr int NS = 4 * SPL;
+  constexpr int NT = FwdStage::NT, RPT = FwdStage::RPT, RSTEP = FwdStage::RSTEP;
+  constexpr int BCN = kTT * NS;
+  constexpr int BCE = (BCN + NT - 1) / NT;
+  constexpr int PF = SSM_FWD_PF;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int c = lane & (kCh - 1);
-  const int hf = lane >> 5;
+  const int c = lane & 15;
+  const int g = lane >> 4;
   const int b = blockIdx.y;
   const int cb = blockIdx.x;
   const int seg = blockIdx.z;
   const int L = p.L, D = p.D, N = p.N;
   const int t_lo = seg * p.seg_len;
   const int t_hi = min(L, t_lo + p.seg_len);
-  const int d = cb * kCh + c;
+  const int cw = wave * 16 + c;
+  const int d = cb * kBlkCh + cw;
   const bool valid = d < D;
   const int dc = valid ? d : 0;
-  const int n0 = wave * kSPW + 2 * hf;
-  const int scol = tid & (kCh - 1);
-  const int srow0 = tid / kCh;
-  const int sd = cb * kCh + scol;
+  const int scol = tid & (kBlkCh - 1);
+  const int srow0 = tid / kBlkCh;
+  const int sd = cb * kBlkCh + scol;
   const bool svalid = sd < D;
   const int sdc = svalid ? sd : 0;
 
-  float A2[2], H[2] = {0.0f, 0.0f}, P[2] = {1.0f, 1.0f};
-  bool live[2];
+  float A2[SPL], H[SPL], P[SPL];
+  bool live[SPL];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    live[j] = valid && n0 + j < N;
-    A2[j] = live[j] ? p.A[(int64_t)dc * N + n0 + j] * kLog2e : 0.0f;
+  for (int j = 0; j < SPL; ++j) {
+    live[j] = valid && SPL * g + j < N;
+    A2[j] = live[j] ? p.A[dc * N + SPL * g + j] * kLog2e : 0.0f;
+    H[j] = 0.0f;
+    P[j] = 1.0f;
   }
 
-  __shared__ float s_u[2][kTT][kCh], s_dt[2][kTT][kCh];
+  __shared__ float2 s_ud[2][kTT][kBlkCh];
   __shared__ __attribute__((aligned(16))) float s_B[2][kTT][NS];
-  __shared__ int s_alive[2][NG];
+  __shared__ int s_alive[2][kFwdWaves];
 
   const int dtD = p.dstride ? D : 1;
   const int scol_dt = p.dstride ? sdc : 0;
@@ -413,14 +478,10 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_agg_k
 #pragma unroll
     for (int k = 0; k < BCE; ++k) {
       const int e = tid + k * NT;
-      int gi;
-      if (NS == N) {
-        gi = t0 * N + e;
-      } else {
-        const int i = e / NS, n = e - i * NS;
-        gi = (t0 + i) * N + min(n, N - 1);
+      if (BCN % NT == 0 || e < BCN) {
+        const int i = e / NS, n = e - (e / NS) * NS;
+        r_B[k] = ld32(B_b, (uint32_t)min((t0 + i) * N + min(n, N - 1), LN - 1));
       }
-      r_B[k] = ld32(B_b, (uint32_t)min(gi, LN - 1));
     }
   };
   auto commit = [&](int buf, int t0) {
@@ -428,14 +489,15 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_agg_k
     for (int k = 0; k < RPT; ++k) {
       const int i = srow0 + k * RSTEP;
       const bool in = svalid && t0 + i < L;
-      s_u[buf][i][scol] = in ? r_u[k] : 0.0f;
-      s_dt[buf][i][scol] = in ? (SP ? softplus(r_dt[k]) : r_dt[k]) : 0.0f;
+      s_ud[buf][i][scol] = in ? make_float2(r_u[k], SP ? softplus(r_dt[k]) : r_dt[k]) : make_float2(0.0f, 0.0f);
     }
 #pragma unroll
     for (int k = 0; k < BCE; ++k) {
       const int e = tid + k * NT;
-      const int i = e / NS, n = e - (e / NS) * NS;
-      (&s_B[buf][0][0])[e] = (t0 + i < L && n < N) ? r_B[k] : 0.0f;
+      if (BCN % NT == 0 || e < BCN) {
+        const int i = e / NS, n = e - (e / NS) * NS;
+        (&s_B[buf][0][0])[e] = (t0 + i < L && n < N) ? r_B[k] : 0.0f;
+      }
     }
   };
 
@@ -447,43 +509,42 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_fwd_agg_k
   for (int t0 = t_last;; t0 -= kTT, buf ^= 1) {
     const bool more = t0 > t_lo;
     if (more) fetch(t0 - kTT);
-    const int tn = min(kTT, L - t0);
-    auto tile = [&](auto full_tag) {
-      constexpr bool kFull = decltype(full_tag)::value;
-      float uu[kTT], dd[kTT];
-#pragma unroll
-      for (int i = 0; i < kTT; ++i) {
-        if (kFull || i < tn) {
-          uu[i] = s_u[buf][i][c];
-          dd[i] = s_dt[buf][i][c];
-        }
-      }
-#pragma unroll
-      for (int i = kTT - 1; i >= 0; --i) {
-        if (kFull || i < tn) {
-          const float2 Bv = *reinterpret_cast<const float2*>(&s_B[buf][i][n0]);
-          const float w = dd[i] * uu[i];
-          H[0] = fmaf(P[0], Bv.x * w, H[0]);
-          H[1] = fmaf(P[1], Bv.y * w, H[1]);
-          P[0] *= fast_exp2(A2[0] * dd[i]);
-          P[1] *= fast_exp2(A2[1] * dd[i]);
-        }
-      }
+    constexpr int R = PF + 1;
+    float2 ud[R];
+    float Bq[R][SPL];
+    auto pre = [&](int i) {
+      ud[i % R] = s_ud[buf][i][cw];
+      lds_vec<SPL>(&s_B[buf][i][SPL * g], Bq[i % R]);
     };
-    if (tn == kTT) tile(std::true_type{}); else tile(std::false_type{});
+#pragma unroll
+    for (int k = 0; k < PF; ++k) pre(kTT - 1 - k);
+#pragma unroll
+    for (int i = kTT - 1; i >= 0; --i) {
+      if (i - PF >= 0) pre(i - PF);
+      __builtin_amdgcn_sched_barrier(0);
+      const float uu = ud[i % R].x, dd = ud[i % R].y;
+      const float w = dd * uu;
+#pragma unroll
+      for (int j = 0; j < SPL; ++j) {
+        H[j] = fmaf(P[j], Bq[i % R][j] * w, H[j]);
+        P[j] *= fast_exp2(A2[j] * dd);
+      }
+    }
     if (more) commit(buf ^ 1, t0 - kTT);
     // products below the smallest normal float are flushed to zero; every
     // earlier step then adds an exact zero, so the walk ends once all are 0
     flush_tiny(P);
-    const bool alive = (live[0] && P[0] != 0.0f) || (live[1] && P[1] != 0.0f);
-    if (!barrier_any<NG>(alive, s_alive[buf]) || !more) break;
+    bool alive = false;
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) alive = alive || (live[j] && P[j] != 0.0f);
+    if (!barrier_any<kFwdWaves>(alive, s_alive[buf]) || !more) break;
   }
   const int64_t o = (int64_t)b * p.nseg + seg;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < SPL; ++j) {
     if (live[j]) {
-      p.agg_H[(o * N + n0 + j) * D + d] = H[j];
-      p.agg_P[(o * N + n0 + j) * D + d] = P[j];
+      p.agg_H[(o * N + SPL * g + j) * D + d] = H[j];
+      p.agg_P[(o * N + SPL * g + j) * D + d] = P[j];
     }
   }
 }
@@ -518,188 +579,214 @@ struct BwdArgs {
   uint32_t flags;
 };
 
-template <int NG, bool EPI, typename T>
-__global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kernel(BwdArgs<T> p) {
-  constexpr int NS = NG * kSPW;
-  constexpr int NT = kWave * NG;
-  constexpr int RPT = kCK * kCh / NT;
-  constexpr int RSTEP = NT / kCh;
-  constexpr int BCE = kCK * NS / NT;
-  static_assert(BCE * NT == kCK * NS && RPT * NT == kCK * kCh, "staging must tile exactly");
-  // dB and dC sums over the 32 channels of a wave half: through an LDS
-  // transpose tile (LDS_DB / LDS_DC) or in registers with cross-lane moves
-  constexpr bool kDbLds = SSM_LDS_DB != 0;
-  constexpr bool kDcLds = SSM_LDS_DC != 0;
-  // steps per batched dB / dC reduction (the fused-epilogue build stages more
-  // operands in LDS and keeps a smaller tile, to stay at 2 workgroups per CU)
-  constexpr int kRB = EPI ? 4 : SSM_BWD_RB;
-  static_assert(kCK % kRB == 0, "reduction batches must tile the block");
+// Staging of a backward block (kCK steps x 64 channels) by the 512 threads:
+// thread -> column scol, rows srow0 + k*8, k < 2.
+struct BwdStage {
+  static constexpr int NT = kWave * kBwdWaves;
+  static constexpr int RPT = kCK * kBlkCh / NT;
+  static constexpr int RSTEP = NT / kBlkCh;
+};
+
+// Workgroup (cb, b, seg) walks the blocks of time segment seg of its 64
+// channels in reverse, starting from the adjoint carry the later segments
+// hand over (ssm_bwd_agg_kernel), and writes du, ddelta, dz and the partial
+// sums of dB, dC, dA, dD (and of a broadcast ddelta).
+// SPL: states per lane (N <= 8 * SPL).  EPI: the gate and the reverse skip.
+// BC: delta is (B,L,1), shared by the channels.
+template <int SPL, bool EPI, bool BC, typename T>
+__global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T> p) {
+  constexpr int NS = 8 * SPL;
+  constexpr int NT = BwdStage::NT, RPT = BwdStage::RPT, RSTEP = BwdStage::RSTEP;
+  constexpr int BCN = kCK * NS;
+  constexpr int BCE = (BCN + NT - 1) / NT;
   constexpr int EB = EPI ? 2 : 1;
   constexpr int ER = EPI ? kCK : 1;
+  constexpr int PF = SSM_BWD_PF;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int c = lane & (kCh - 1);
-  const int hf = lane >> 5;
+  const int c = lane & 7;
+  const int g = lane >> 3;
   const int b = blockIdx.y;
   const int cb = blockIdx.x;
   const int seg = blockIdx.z;
   const int L = p.L, D = p.D, N = p.N;
   const int blk_lo = seg * (p.seg_len / kCK);
   const int blk_hi = min(p.nblk, blk_lo + p.seg_len / kCK);
-  const int d = cb * kCh + c;
+  const int cw = wave * 8 + c;
+  const int d = cb * kBlkCh + cw;
   const bool valid = d < D;
   const int dc = valid ? d : 0;
-  const int n0 = wave * kSPW + 2 * hf;
+  const int sig = chan_sig<SPL>(c);
+  int nj[SPL];  // state of slot j
+#pragma unroll
+  for (int j = 0; j < SPL; ++j) nj[j] = SPL * g + (j ^ sig);
   const bool rev = p.flags & SSM_REVERSE;
   const bool comp = rev && (p.flags & SSM_COMPLEMENT);
   const bool gate = EPI && (p.flags & SSM_GATE);
   const bool skip = (p.flags & SSM_SKIP) != 0;  // non-EPI builds run only the forward-scan skip
-  const bool stage_dyo = EPI && skip && rev;  // gated dy at the unmirrored (t,d) for the skip term
-  const bool stage_eu = gate && skip && rev;  // u at the output position for y_pre
+  const bool stage_dyo = EPI && skip && rev;    // gated dy at the unmirrored (t,d) for the skip term
+  const bool stage_eu = gate && skip && rev;    // u at the output position for y_pre
   const bool dsp = p.flags & SSM_DELTA_SOFTPLUS;
-  const int scol = tid & (kCh - 1);
-  const int srow0 = tid / kCh;
-  const int sd = cb * kCh + scol;
+  const int q = comp ? D - 1 - dc : dc;
+  const float Dd = (skip && valid) ? p.Dskip[dc] : 0.0f;  // y_out[t,d] holds u[t,d] D[d] (selectssm.py:238)
+  const float Dq = (skip && valid) ? p.Dskip[q] : 0.0f;   // the skip inside y_pre at the output position
+  const int scol = tid & (kBlkCh - 1);
+  const int srow0 = wave;  // = tid / kBlkCh: the staged rows of a wave are uniform
+  const int sd = cb * kBlkCh + scol;
   const bool svalid = sd < D;
-  const bool full_cb = (cb + 1) * kCh <= D;
   const int sdc = svalid ? sd : 0;
   const int sq = comp ? D - 1 - sdc : sdc;
-  const float Dd = (skip && svalid) ? p.Dskip[sdc] : 0.0f;
-  const float Dq = (skip && svalid) ? p.Dskip[sq] : 0.0f;
+  const bool full_cb = (cb + 1) * kBlkCh <= D;
+  // after the exchange over state groups, row g >> 1 of the wave holds
+  // du (rows 0, 1) or ddelta (rows 2, 3) of one of 2 steps, twice (both halves)
+  const int orow = g >> 1;
+  const bool is_du = orow < 2;
+  const bool lead = (g & 1) == 0;
+  const float Ddu = is_du ? Dd : 0.0f;                  // the skip's du term, on du rows
+  const float dmask = (is_du && lead) ? 1.0f : 0.0f;    // one lane per (step, channel) adds to dD
+  // du / ddelta of step t0 + i + (1 - (orow & 1)) go to row t0 + i plus this offset
+  const uint32_t oo = (uint32_t)((1 - (orow & 1)) * D + d);  // elements
+  // dz of step t0 + i - 3 + yrow_step(orow): row t0 + i - 3 (or L-1-(t0+i)) plus this offset
+  const uint32_t dzo = (uint32_t)(((rev ? 3 - yrow_step(orow) : yrow_step(orow)) * D + q) * sizeof(T));
 
-  float Av[2], A2[2], g[2], dAacc[2];
+  float Av[SPL], A2[SPL], gc[SPL], dAacc[SPL], dAmid[SPL];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int n = n0 + j;
-    Av[j] = (valid && n < N) ? p.A[(int64_t)dc * N + n] : 0.0f;
+  for (int j = 0; j < SPL; ++j) {
+    Av[j] = (valid && nj[j] < N) ? p.A[dc * N + nj[j]] : 0.0f;
     A2[j] = Av[j] * kLog2e;
-    g[j] = 0.0f;
+    gc[j] = 0.0f;
     dAacc[j] = 0.0f;
+    dAmid[j] = 0.0f;
   }
   if (seg < p.nseg - 1) {
     // adjoint carry entering this segment from the right: g = P g + G over the
     // later segments, last segment first (g = a_t f_t at each segment's first
     // step is linear in the carry it receives)
     const int64_t base = (int64_t)b * p.nseg * N * D + dc;
-    const int nc0 = min(n0, N - 1), nc1 = min(n0 + 1, N - 1);
-#pragma unroll 4
+#pragma unroll 2
     for (int s = p.nseg - 1; s > seg; --s) {
-      const int64_t o0 = base + ((int64_t)s * N + nc0) * D, o1 = base + ((int64_t)s * N + nc1) * D;
-      g[0] = fmaf(p.agg_P[o0], g[0], p.agg_G[o0]);
-      g[1] = fmaf(p.agg_P[o1], g[1], p.agg_G[o1]);
+#pragma unroll
+      for (int j = 0; j < SPL; ++j) {
+        const int64_t o = base + ((int64_t)s * N + min(nj[j], N - 1)) * D;
+        gc[j] = fmaf(p.agg_P[o], gc[j], p.agg_G[o]);
+      }
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      if (!(valid && n0 + j < N)) g[j] = 0.0f;
+    for (int j = 0; j < SPL; ++j)
+      if (!(valid && nj[j] < N)) gc[j] = 0.0f;
   }
   // dA and dD are sums over every step of the row: per block (16 steps), per
   // group of 16 blocks, then the total, so a 2^20-step row's total sees 4096
   // fp32 adds instead of 2^20
-  float dAmid[2] = {0.0f, 0.0f};
-  float dDacc = 0.0f;  // for column scol, over this thread's rows
-  float dDmid = 0.0f;
+  float dDacc = 0.0f, dDmid = 0.0f;
 
-  __shared__ float s_u[2][kCK][kCh], s_dt[2][kCK][kCh], s_dy[2][kCK][kCh];
-  __shared__ float s_go[EB][ER][kCh], s_gz[EB][ER][kCh];  // gate: raw dy and z at the output position
-  __shared__ float s_eu[EB][ER][kCh], s_dyo[EB][ER][kCh];
-  __shared__ __attribute__((aligned(16))) float s_B[2][kCK][NS];
-  __shared__ __attribute__((aligned(16))) float s_C[2][kCK][NS];
-  __shared__ float s_sig[2][kCK][kCh];                 // softplus'(delta) = sigmoid(delta) (SSM_DELTA_SOFTPLUS)
-  __shared__ float sbuf[NG][kCK][kWave];               // [du | ddelta] per wave
-  __shared__ float ybuf[EPI ? NG : 1][EPI ? kCK : 1][kCh];  // (gate) y of each wave's states, per channel
-  __shared__ float bcbuf[2][kCK][NS];                  // dB, dC totals of this channel block
-  __shared__ float bdummy[2][kWave];                   // sink for lanes without a total
-  // per wave: the dB (or dC) values of kRB steps, one row of 32 channels per
-  // (step, state slot, half), summed row-wise every kRB steps
-  __shared__ __attribute__((aligned(16))) float rbuf[NG][kRB * 4][kRS];
+  __shared__ float4 s_x[2][kCK][kBlkCh];  // (u, delta, dy of the scan, softplus'(delta) or 1)
+  // (B, C) of each step in the state order of each lane class: [t][group][sig][B slots, C slots]
+  __shared__ __attribute__((aligned(16))) float s_bc[2][kCK][8][SPL][2 * SPL];
+  __shared__ float s_dB[kBwdWaves][kCK][NS], s_dC[kBwdWaves][kCK][NS];  // per-wave channel sums
+  __shared__ float s_go[EB][ER][kBlkCh], s_gz[EB][ER][kBlkCh];  // gate: raw dy and z at the output position
+  __shared__ float s_eu[EB][ER][kBlkCh], s_dyo[EB][ER][kBlkCh];
+  __shared__ float s_ddt[kBwdWaves][kCK];  // broadcast delta: per-wave channel sums of ddelta
 
-  const int64_t bLD = (int64_t)b * L * D;
-  const int64_t bLN = (int64_t)b * L * N;
   const int dtD = p.dstride ? D : 1;
-  const int64_t bLDt = (int64_t)b * L * dtD;
   const int scol_dt = p.dstride ? sdc : 0;
-  const T* __restrict__ u_b = p.u + bLD;
-  const T* __restrict__ dt_b = p.delta + bLDt;
+  const T* __restrict__ u_b = p.u + (int64_t)b * L * D;
+  const T* __restrict__ dt_b = p.delta + (int64_t)b * L * dtD;
   const int ldy = p.ldy, ldz = p.ldz;
   const T* __restrict__ dy_b = p.dy + (int64_t)b * L * ldy;
   const T* __restrict__ z_b = EPI ? p.z + (int64_t)b * L * ldz : nullptr;
-  const T* __restrict__ B_b = p.Bc + bLN;
-  const T* __restrict__ C_b = p.Cc + bLN;
+  const T* __restrict__ B_b = p.Bc + (int64_t)b * L * N;
+  const T* __restrict__ C_b = p.Cc + (int64_t)b * L * N;
   const float* __restrict__ ck_b = p.ckpt + (int64_t)b * p.nblk * N * D;
-  T* __restrict__ du_b = p.du + bLD;
-  T* __restrict__ ddt_b = p.ddelta + bLD;  // only used when delta is (B,L,D)
-  T* __restrict__ dz_b = EPI ? p.dz + bLD : nullptr;
+  T* __restrict__ out_b = (is_du ? p.du : p.ddelta) + (int64_t)b * L * D;  // ddelta only when (B,L,D)
+  T* __restrict__ dz_b = EPI ? p.dz + (int64_t)b * L * D : nullptr;
   const int LN = L * N;
 
   // fetch() only issues loads; commit() (after the block's compute) masks,
-  // applies the gate and writes LDS
+  // applies softplus and the gate and writes LDS
   float r_u[RPT], r_dt[RPT], r_dy[RPT], r_gz[RPT], r_eu[RPT], r_dyo[RPT], r_zo[RPT];
-  float r_B[BCE], r_C[BCE], r_h[2];
+  float r_B[BCE], r_C[BCE], r_h[SPL];
+  float h_next[SPL];  // checkpoint of the block staged by the last commit
+  // byte offsets of this thread's staged column in a u row and an output row
+  const uint32_t so_c = (uint32_t)(sdc * sizeof(T));
+  const uint32_t so_q = (uint32_t)(sq * sizeof(T));
+  const uint32_t so_dt = (uint32_t)(scol_dt * sizeof(T));
+  const buf_t ru = make_buf(u_b), rdt = make_buf(dt_b), rdy = make_buf(dy_b), rB = make_buf(B_b), rC = make_buf(C_b);
+  const buf_t rck = make_buf(ck_b), rdz = make_buf(EPI ? dz_b : p.du);
+  const uint32_t rowb = (uint32_t)(D * sizeof(T));      // bytes per (B,L,D) row
+  const uint32_t dyrowb = (uint32_t)(ldy * sizeof(T));  // bytes per dy row
+  const uint32_t ckrowb = (uint32_t)(N * D * sizeof(float));
+  uint32_t cko[SPL];  // checkpoint offsets of this lane's states within a block
+#pragma unroll
+  for (int j = 0; j < SPL; ++j) cko[j] = (uint32_t)((min(nj[j], N - 1) * D + dc) * sizeof(float));
   auto fetch = [&](int blk) {
     const int t0 = blk * kCK;
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
-      const int tc = min(t0 + srow0 + k * RSTEP, L - 1);
-      const int pr = rev ? L - 1 - tc : tc;  // output row of scan step tc
-      r_u[k] = ld32(u_b, (uint32_t)(tc * D + sdc));
-      r_dt[k] = ld32(dt_b, (uint32_t)(tc * dtD + scol_dt));
-      r_dy[k] = ld32(dy_b, (uint32_t)(pr * ldy + sq));
-      if (gate) r_gz[k] = ld32(z_b, (uint32_t)(pr * ldz + sq));
-      if (stage_eu) r_eu[k] = ld32(u_b, (uint32_t)(pr * D + sq));
-      if (stage_dyo) {
-        r_dyo[k] = ld32(dy_b, (uint32_t)(tc * ldy + sdc));
-        if (gate) r_zo[k] = ld32(z_b, (uint32_t)(tc * ldz + sdc));
-      }
+      const int tc = min(t0 + srow0 + k * RSTEP, L - 1);  // wave-uniform
+      const int pr = rev ? L - 1 - tc : tc;              // output row of scan step tc
+      r_u[k] = bld<T>(ru, so_c, (uint32_t)tc * rowb);
+      r_dt[k] = bld<T>(rdt, so_dt, (uint32_t)(tc * dtD * sizeof(T)));
+      r_dy[k] = bld<T>(rdy, so_q, (uint32_t)pr * dyrowb);
     }
 #pragma unroll
     for (int k = 0; k < BCE; ++k) {
       const int e = tid + k * NT;
-      int gi;
-      if (NS == N) {
-        gi = t0 * N + e;
-      } else {
-        const int i = e / NS, n = e - i * NS;
-        gi = (t0 + i) * N + min(n, N - 1);
+      if (BCN % NT == 0 || e < BCN) {
+        const int i = e / NS, n = e - (e / NS) * NS;
+        const uint32_t o = (uint32_t)(min((t0 + i) * N + min(n, N - 1), LN - 1) * sizeof(T));
+        r_B[k] = bld<T>(rB, o, 0);
+        r_C[k] = bld<T>(rC, o, 0);
       }
-      const int gc = min(gi, LN - 1);
-      r_B[k] = ld32(B_b, (uint32_t)gc);
-      r_C[k] = ld32(C_b, (uint32_t)gc);
+    }
+    if (gate || stage_eu || stage_dyo) {
+#pragma unroll
+      for (int k = 0; k < RPT; ++k) {
+        const int tc = min(t0 + srow0 + k * RSTEP, L - 1);
+        const int pr = rev ? L - 1 - tc : tc;
+        if (gate) r_gz[k] = ld32(z_b, (uint32_t)(pr * ldz + sq));
+        if (stage_eu) r_eu[k] = ld32(u_b, (uint32_t)(pr * D + sq));
+        if (stage_dyo) {
+          r_dyo[k] = ld32(dy_b, (uint32_t)(tc * ldy + sdc));
+          if (gate) r_zo[k] = ld32(z_b, (uint32_t)(tc * ldz + sdc));
+        }
+      }
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) r_h[j] = ld32(ck_b, (uint32_t)((blk * N + min(n0 + j, N - 1)) * D + dc));
+    for (int j = 0; j < SPL; ++j) r_h[j] = bld<float>(rck, cko[j], (uint32_t)blk * ckrowb);
   };
   // softplus(delta) and its derivative: a separate copy of the staging loop
-  auto stage_dt = [&](int buf, int t0, auto sp_tag) {
+  auto stage_x = [&](int buf, int t0, auto sp_tag) {
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
       const int i = srow0 + k * RSTEP;
       const bool in = svalid && t0 + i < L;
+      float dtv = r_dt[k], sg = 1.0f;
       if constexpr (decltype(sp_tag)::value) {
-        s_dt[buf][i][scol] = in ? softplus(r_dt[k]) : 0.0f;
-        s_sig[buf][i][scol] = in ? sigmoid(r_dt[k]) : 0.0f;
-      } else {
-        s_dt[buf][i][scol] = in ? r_dt[k] : 0.0f;
+        sg = sigmoid(dtv);
+        dtv = softplus(dtv);
       }
-    }
-  };
-  auto commit = [&](int buf, int blk) {
-    const int t0 = blk * kCK;
-    if (dsp) stage_dt(buf, t0, std::true_type{}); else stage_dt(buf, t0, std::false_type{});
-#pragma unroll
-    for (int k = 0; k < RPT; ++k) {
-      const int i = srow0 + k * RSTEP;
-      const bool in = svalid && t0 + i < L;
-      s_u[buf][i][scol] = in ? r_u[k] : 0.0f;
       const float go = in ? r_dy[k] : 0.0f;
+      float dyg = go;
       if (gate) {
         const float gz = in ? r_gz[k] : 0.0f;
         s_go[buf][i][scol] = go;
         s_gz[buf][i][scol] = gz;
-        s_dy[buf][i][scol] = go * gz * sigmoid(gz);
-      } else {
-        s_dy[buf][i][scol] = go;
+        dyg = go * gz * sigmoid(gz);
       }
+      s_x[buf][i][scol] = in ? make_float4(r_u[k], dtv, dyg, sg) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+  };
+  auto commit = [&](int buf, int blk) {
+    const int t0 = blk * kCK;
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) h_next[j] = (valid && nj[j] < N) ? r_h[j] : 0.0f;
+    if (dsp) stage_x(buf, t0, std::true_type{}); else stage_x(buf, t0, std::false_type{});
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      const int i = srow0 + k * RSTEP;
+      const bool in = svalid && t0 + i < L;
       if (stage_eu) s_eu[buf][i][scol] = in ? r_eu[k] : 0.0f;
       if (stage_dyo) {
         float v = in ? r_dyo[k] : 0.0f;
@@ -713,10 +800,17 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
 #pragma unroll
     for (int k = 0; k < BCE; ++k) {
       const int e = tid + k * NT;
-      const int i = e / NS, n = e - (e / NS) * NS;
-      const bool in = t0 + i < L && n < N;
-      (&s_B[buf][0][0])[e] = in ? r_B[k] : 0.0f;
-      (&s_C[buf][0][0])[e] = in ? r_C[k] : 0.0f;
+      if (BCN % NT == 0 || e < BCN) {
+        const int i = e / NS, n = e - (e / NS) * NS;
+        const bool in = t0 + i < L && n < N;
+        const float vb = in ? r_B[k] : 0.0f, vc = in ? r_C[k] : 0.0f;
+        const int gg = n / SPL, jj = n % SPL;
+#pragma unroll
+        for (int s = 0; s < SPL; ++s) {
+          s_bc[buf][i][gg][s][jj ^ s] = vb;
+          s_bc[buf][i][gg][s][SPL + (jj ^ s)] = vc;
+        }
+      }
     }
   };
 
@@ -724,282 +818,189 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
   commit(0, blk_hi - 1);
   __syncthreads();
   int buf = 0;
-  float h[2];
+  float h[SPL];
   for (int blk = blk_hi - 1; blk >= blk_lo; --blk, buf ^= 1) {
     const int t0 = blk * kCK;
-    const int tn = min(kCK, L - t0);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) h[j] = (valid && n0 + j < N) ? r_h[j] : 0.0f;
+    for (int j = 0; j < SPL; ++j) h[j] = h_next[j];
     const bool more = blk > blk_lo;
     if (more) fetch(blk - 1);
-
+    // a full block (every channel exists, no step beyond L) runs without
+    // per-lane predicates
+    const bool full = full_cb && t0 + kCK <= L;
+    float dAblk[SPL];
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) dAblk[j] = 0.0f;
+    float dDblk = 0.0f;
     auto sweeps = [&](auto full_tag) {
       constexpr bool kFull = decltype(full_tag)::value;
-      float a_s[kCK][2], hp_s[kCK][2];
-      float uu[kCK], dd[kCK], dyv[kCK];
+      float a_s[kCK][SPL], hp_s[kCK][SPL];
+      constexpr int R = PF + 1;  // ring of operand sets, steps i .. i +- PF
+      float4 xr[R];
+      float bc[R][2 * SPL];
+      auto pre = [&](int i) {
+        xr[i % R] = s_x[buf][i][cw];
+        lds_vec<2 * SPL>(&s_bc[buf][i][g][sig][0], bc[i % R]);
+      };
+      // forward recompute of the block: a_t, h_{t-1}; dC_t = sum_d dy_t h_t;
+      // with the gate, y_t for dz
+#pragma unroll
+      for (int i = 0; i < PF; ++i) pre(i);
+      float yp[4];
 #pragma unroll
       for (int i = 0; i < kCK; ++i) {
-        if (kFull || i < tn) {
-          uu[i] = s_u[buf][i][c];
-          dd[i] = s_dt[buf][i][c];
-          dyv[i] = s_dy[buf][i][c];
+        if (i + PF < kCK) pre(i + PF);
+        __builtin_amdgcn_sched_barrier(0);
+        const float uu = xr[i % R].x, dd = xr[i % R].y, dyv = xr[i % R].z;
+        const float w = dd * uu;
+        float vC[SPL];
+#pragma unroll
+        for (int j = 0; j < SPL; ++j) {
+          const float a = fast_exp2(A2[j] * dd);
+          a_s[i][j] = a;
+          hp_s[i][j] = h[j];
+          h[j] = fmaf(a, h[j], bc[i % R][j] * w);
+          vC[j] = dyv * h[j];
         }
-      }
-      // dB / dC: lane (c, hf) writes its two values of step i into rows
-      // ((i % kRB) * 2 + slot) * 2 + hf of its wave's tile.  When a batch of
-      // kRB steps is written, lane l reads its part of row l % kRows with
-      // float4 loads; two steps later it sums them, the parts are added across
-      // lanes, and lanes < kRows write the totals (the others a per-lane dummy
-      // slot).  LDS operations of one wave execute in order and the compiler
-      // keeps the tile's (possibly aliasing) writes and reads in program
-      // order, so no barrier or wait is needed between them.
-      // B_t and C_t are read kPF steps ahead of use, before the tile writes
-      // of the steps in between, so their latency is covered as well.
-      float(*tile)[kRS] = rbuf[wave];
-      auto put = [&](int i, float v0, float v1) {
-        tile[((i % kRB) * 2 + 0) * 2 + hf][c] = v0;
-        tile[((i % kRB) * 2 + 1) * 2 + hf][c] = v1;
-      };
-      constexpr int kRows = kRB * 4;            // 64, 32 or 16 rows
-      constexpr int kPer = 32 * kRows / kWave;  // values of a row per lane: 32, 16 or 8
-      float4 pq[kPer / 4];
-      auto flush_issue = [&]() {
-        const float4* src = reinterpret_cast<const float4*>(&tile[lane % kRows][kPer * (lane / kRows)]);
+        s_dC[wave][i][SPL * g + sig] = chan_reduce8<SPL>(vC);
+        if (gate) {
+          float ys = bc[i % R][SPL] * h[0];
 #pragma unroll
-        for (int k = 0; k < kPer / 4; ++k) pq[k] = src[k];
-      };
-      auto flush_finish = [&](int i0, int qsel) {
-        float v = 0.0f;
-#pragma unroll
-        for (int k = 0; k < kPer / 4; ++k) v += (pq[k].x + pq[k].y) + (pq[k].z + pq[k].w);
-        if constexpr (kRows == 16) {  // lanes l, l ^ 16 hold parts of one row
-          auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-          v = __uint_as_float(s16[0]) + __uint_as_float(s16[1]);
-        }
-        if constexpr (kRows < kWave) {  // lanes l, l ^ 32 hold parts of one row
-          auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-          v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-        }
-        const int r = lane % kRows;
-        const int n = wave * kSPW + 2 * (r & 1) + ((r >> 1) & 1);
-        float* dst = lane < kRows ? &bcbuf[qsel][i0 + (r >> 2)][n] : &bdummy[qsel][lane];
-        *dst = v;
-      };
-      // register path: 4 steps x 2 states summed together with cross-lane moves
-      float xb[4][2];
-      auto xflush = [&](int i0, int qsel) {
-        float x8[8];
-#pragma unroll
-        for (int m = 0; m < 8; ++m) x8[m] = xb[m >> 1][m & 1];
-        const float r = reduce32x8(x8);
-        const int v = reduce32x8_value(lane);
-        const int n = wave * kSPW + 2 * reduce32x8_half(lane) + (v & 1);
-        float* dst = (lane & 3) == 0 ? &bcbuf[qsel][i0 + (v >> 1)][n] : &bdummy[qsel][lane];
-        *dst = r;
-      };
-      // steps ahead that B / C are read (the fused-epilogue build has fewer
-      // registers to spare)
-      constexpr int kPF = EPI ? 1 : SSM_BWD_PF;
-      float2 Bl[kCK], Cl[kCK];
-      auto ldB = [&](int i) { Bl[i] = *reinterpret_cast<const float2*>(&s_B[buf][i][n0]); };
-      auto ldC = [&](int i) { Cl[i] = *reinterpret_cast<const float2*>(&s_C[buf][i][n0]); };
-      float yp[kCK];  // (gate) this lane's part of y, per step
-      // forward recompute of the block: a_t, h_{t-1}; dC_t = sum_d dy_t h_t
-#pragma unroll
-      for (int i = 0; i < kPF; ++i) {
-        ldB(i);
-        if (gate) ldC(i);
-      }
-#pragma unroll
-      for (int i = 0; i < kCK; ++i) {
-        if (i + kPF < kCK) {
-          ldB(i + kPF);
-          if (gate) ldC(i + kPF);
-        }
-        if (kFull || i < tn) {
-          const float w = dd[i] * uu[i];
-          const float Bn[2] = {Bl[i].x, Bl[i].y};
-#pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const float a = fast_exp2(A2[j] * dd[i]);
-            a_s[i][j] = a;
-            hp_s[i][j] = h[j];
-            h[j] = fmaf(a, h[j], Bn[j] * w);
-          }
-          if constexpr (kDcLds) {
-            put(i, dyv[i] * h[0], dyv[i] * h[1]);
-          } else {
-            xb[i % 4][0] = dyv[i] * h[0];
-            xb[i % 4][1] = dyv[i] * h[1];
-          }
-          if (gate) {
-            yp[i] = fmaf(Cl[i].y, h[1], Cl[i].x * h[0]);
-            // steps i-1, i: the halves' sums land in lanes < 32 (even step) and >= 32 (odd);
-            // a partial block's last step, if even, is paired with nothing
-            if (i & 1) {
-              ybuf[EPI ? wave : 0][EPI ? i - 1 + hf : 0][c] = half_pair(yp[i - 1], yp[i]);
-            } else if (!kFull && i == tn - 1) {
-              ybuf[EPI ? wave : 0][EPI ? i + hf : 0][c] = half_pair(yp[i], 0.0f);
+          for (int j = 1; j < SPL; ++j) ys = fmaf(bc[i % R][SPL + j], h[j], ys);
+          yp[i & 3] = ys;
+          if ((i & 3) == 3) {
+            float yv = rows_transpose_sum4(yp[0], yp[1], yp[2], yp[3]);
+            yv += dpp_mov<kDppRor8>(yv);
+            const int ti = i - 3 + yrow_step(orow);
+            const int t = t0 + ti;
+            if (skip) yv = fmaf(stage_eu ? s_eu[buf][ti][cw] : s_x[buf][ti][cw].x, Dq, yv);
+            const float zz = s_gz[buf][ti][cw];
+            const float sg = sigmoid(zz);
+            const float dzv = s_go[buf][ti][cw] * yv * sg * (1.0f + zz * (1.0f - sg));
+            // both halves of the row hold the value; both store it
+            if constexpr (kFull) {
+              bst<T>(rdz, dzo, (uint32_t)(rev ? L - 1 - t0 - i : t0 + i - 3) * rowb, dzv);
+            } else if (valid && t < L) {
+              bst<T>(rdz, (uint32_t)(rev ? L - 1 - t : t) * rowb + (uint32_t)(q * sizeof(T)), 0, dzv);
             }
           }
-        }
-        // batches are flushed whole: a partial block's rows beyond tn give totals nobody reads
-        if constexpr (kDcLds) {
-          if (i % kRB == kRB - 1) flush_issue();
-          if (i % kRB == 1 && i > kRB) flush_finish(i - 1 - kRB, 1);
-        } else {
-          if (!kFull && i >= tn) xb[i % 4][0] = xb[i % 4][1] = 0.0f;
-          if (i % 4 == 3) xflush(i - 3, 1);
         }
       }
       // adjoint, backwards through the block
-      float dAblk[2] = {0.0f, 0.0f};
+      float v1p = 0.0f, v2p = 0.0f;
 #pragma unroll
-      for (int i = 0; i < kPF; ++i) {
-        ldB(kCK - 1 - i);
-        ldC(kCK - 1 - i);
-      }
+      for (int k = 0; k < PF; ++k) pre(kCK - 1 - k);
 #pragma unroll
       for (int i = kCK - 1; i >= 0; --i) {
-        if (i >= kPF) {
-          ldB(i - kPF);
-          ldC(i - kPF);
-        }
-        if (kFull || i < tn) {
-          const float Bn[2] = {Bl[i].x, Bl[i].y};
-          const float Cn[2] = {Cl[i].x, Cl[i].y};
-          const float w = dd[i] * uu[i];
-          float s1 = 0.0f, s2 = 0.0f, fw[2];
+        if (i - PF >= 0) pre(i - PF);
+        __builtin_amdgcn_sched_barrier(0);
+        const float uu = xr[i % R].x, dd = xr[i % R].y, dyv = xr[i % R].z;
+        const float w = dd * uu;
+        float s1 = 0.0f, s2 = 0.0f, vB[SPL];
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const float f = fmaf(Cn[j], dyv[i], g[j]);
-            const float gg = a_s[i][j] * f;
-            const float qv = gg * hp_s[i][j];
-            s2 = fmaf(Av[j], qv, s2);
-            dAblk[j] = fmaf(dd[i], qv, dAblk[j]);
-            s1 = fmaf(Bn[j], f, s1);
-            fw[j] = f * w;
-            g[j] = gg;
-          }
-          if constexpr (kDbLds) {
-            put(i, fw[0], fw[1]);
-          } else {
-            xb[i % 4][0] = fw[0];
-            xb[i % 4][1] = fw[1];
-          }
-          // du partial in lanes < 32, ddelta partial in lanes >= 32
-          sbuf[wave][i][lane] = half_pair(dd[i] * s1, fmaf(uu[i], s1, s2));
+        for (int j = 0; j < SPL; ++j) {
+          const float f = fmaf(bc[i % R][SPL + j], dyv, gc[j]);
+          const float gg = a_s[i][j] * f;
+          const float qv = gg * hp_s[i][j];
+          s2 = j == 0 ? Av[0] * qv : fmaf(Av[j], qv, s2);
+          dAblk[j] = fmaf(dd, qv, dAblk[j]);
+          s1 = j == 0 ? bc[i % R][0] * f : fmaf(bc[i % R][j], f, s1);
+          vB[j] = f * w;
+          gc[j] = gg;
         }
-        if constexpr (kDcLds) {
-          if (i == kCK - 3) flush_finish(kCK - kRB, 1);  // the forward sweep's last dC batch
-        }
-        if constexpr (kDbLds) {
-          if (i % kRB == 0) flush_issue();
-          if (i % kRB == kRB - 2 && i < kCK - kRB) flush_finish(i + 2, 0);
+        s_dB[wave][i][SPL * g + sig] = chan_reduce8<SPL>(vB);
+        // du = delta sum_n f B; ddelta = sum_n f (A a h_{t-1} + B u)
+        const float v1 = dd * s1, v2 = fmaf(uu, s1, s2);
+        if (i & 1) {
+          v1p = v1;
+          v2p = v2;
         } else {
-          if (!kFull && i >= tn) xb[i % 4][0] = xb[i % 4][1] = 0.0f;
-          if (i % 4 == 0) xflush(i, 0);
-        }
-      }
-      if constexpr (kDbLds) flush_finish(0, 0);
-      dAmid[0] += dAblk[0];
-      dAmid[1] += dAblk[1];
-    };
-    if (tn == kCK) sweeps(std::true_type{}); else sweeps(std::false_type{});
-    __syncthreads();
-
-    // combine the per-wave partials; write du, ddelta (and dz)
-    auto combine = [&](auto full_tag) {
-      constexpr bool kFull = decltype(full_tag)::value;
-      float dDblk = 0.0f;  // per block, like dA
-#pragma unroll
-      for (int k = 0; k < RPT; ++k) {
-        const int i = srow0 + k * RSTEP;
-        if (kFull || i < tn) {
-          float du = 0.0f, ddt = 0.0f;
-#pragma unroll
-          for (int w = 0; w < NG; ++w) {
-            du += sbuf[w][i][scol];
-            ddt += sbuf[w][i][kCh + scol];
-          }
-          const int t = t0 + i;
-          const float uu = s_u[buf][i][scol];
-          if (dsp) ddt *= s_sig[buf][i][scol];  // through softplus (the same factor for every channel when broadcast)
-          if (skip) {
-            // y_out[t,d] holds u[t,d]*D[d] (selectssm.py:238): its gradient lands on u[t,d]
-            float dyo = s_dy[buf][i][scol];
+          // steps i+1, i summed over the state groups: rows 0, 1 hold du of
+          // steps i+1, i and rows 2, 3 ddelta of steps i+1, i (both halves)
+          float val = row_pair(half_pair(v1p, v2p), half_pair(v1, v2));
+          val += dpp_mov<kDppRor8>(val);
+          const int ti = i + ((orow & 1) ? 0 : 1);
+          const int t = t0 + ti;
+          if (skip || dsp) {
+            // du[t,d] += D[d] dy_out[t,d] and dD[d] += dy_out[t,d] u[t,d] on
+            // du rows (Ddu is 0 without the skip); ddelta through softplus
+            // (x.w is softplus'(delta), or 1)
+            const float4 xo = s_x[buf][ti][cw];
+            float dyo = xo.z;
             if constexpr (EPI) {
-              if (stage_dyo) dyo = s_dyo[buf][i][scol];
+              if (stage_dyo) dyo = s_dyo[buf][ti][cw];
             }
-            du = fmaf(Dd, dyo, du);
-            dDblk = fmaf(dyo, uu, dDblk);
+            val = fmaf(Ddu, dyo, val);
+            dDblk = fmaf(dmask * dyo, xo.x, dDblk);
+            val *= is_du ? 1.0f : xo.w;
           }
-          on_valid_lanes(full_cb, svalid, [&] {
-            st32(du_b, (uint32_t)(t * D + sdc), du);
-            if (p.dstride) st32(ddt_b, (uint32_t)(t * D + sdc), ddt);
-          });
-          if (!p.dstride) {
-            // the 32 threads of this half-wave hold the 32 channels of row i
-            const float tot = half_sum32(svalid ? ddt : 0.0f);
-            if (scol == 0) p.ws_ddt[((int64_t)cb * p.Bt + b) * L + t] = tot;
-          }
-          if (gate && svalid) {
-            float ys = 0.0f;
-#pragma unroll
-            for (int w = 0; w < NG; ++w) ys += ybuf[EPI ? w : 0][EPI ? i : 0][scol];
-            if (skip) ys = fmaf(stage_eu ? s_eu[buf][i][scol] : uu, Dq, ys);
-            const float zz = s_gz[buf][i][scol];
-            const float sg = sigmoid(zz);
-            const int pt = rev ? L - 1 - t : t;
-            st32(dz_b, (uint32_t)(pt * D + sq), s_go[buf][i][scol] * ys * sg * (1.0f + zz * (1.0f - sg)));
+          // du and ddelta rows of the wave store to different tensors: a
+          // per-lane pointer (out_b)
+          const uint32_t ro = (uint32_t)((t0 + i) * D);
+          if constexpr (!BC) {
+            if (kFull || (valid && t < L)) st32(out_b, ro + oo, val);
+          } else {
+            if (is_du && valid && t < L) st32(out_b, ro + oo, val);
+            // one ddelta shared by the channels: sum the wave's 8 channels
+            float sv = val + dpp_mov<kDppHalfMirror>(val);
+            sv += dpp_mov<kDppXor2>(sv);
+            sv += dpp_mov<kDppXor1>(sv);
+            if (!is_du && lead && c == 0) s_ddt[wave][ti] = sv;
           }
         }
       }
-      dDmid += dDblk;
     };
-    if (tn == kCK) combine(std::true_type{}); else combine(std::false_type{});
+    if (full) sweeps(std::true_type{}); else sweeps(std::false_type{});
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) dAmid[j] += dAblk[j];
+    dDmid += dDblk;
     if (((blk - blk_lo) & 15) == 0) {  // close a group of 16 blocks (and the row's last group)
-      dAacc[0] += dAmid[0];
-      dAacc[1] += dAmid[1];
-      dDacc += dDmid;
-      dAmid[0] = dAmid[1] = dDmid = 0.0f;
-    }
-    // dB, dC totals of this channel block, coalesced
-    {
-      float* __restrict__ wB = p.ws_dB + (((int64_t)cb * p.Bt + b) * L + t0) * N;
-      float* __restrict__ wC = p.ws_dC + (((int64_t)cb * p.Bt + b) * L + t0) * N;
-      for (int idx = tid; idx < tn * N; idx += NT) {
-        int i, n;
-        if (NS == N) {
-          i = idx / NS;
-          n = idx - i * NS;
-        } else {
-          i = idx / N;
-          n = idx - i * N;
-        }
-        wB[idx] = bcbuf[0][i][n];
-        wC[idx] = bcbuf[1][i][n];
+#pragma unroll
+      for (int j = 0; j < SPL; ++j) {
+        dAacc[j] += dAmid[j];
+        dAmid[j] = 0.0f;
       }
+      dDacc += dDmid;
+      dDmid = 0.0f;
+    }
+    __syncthreads();
+    // dB, dC totals of this channel block: the 8 waves' sums added in order
+    for (int e = tid; e < 2 * kCK * NS; e += NT) {
+      const int which = e / (kCK * NS);
+      const int r = e - which * (kCK * NS);
+      const int i = r / NS, n = r - (r / NS) * NS;
+      if (n < N && t0 + i < L) {
+        float s = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kBwdWaves; ++w) s += which ? s_dC[w][i][n] : s_dB[w][i][n];
+        float* dst = which ? p.ws_dC : p.ws_dB;
+        dst[(((int64_t)cb * p.Bt + b) * L + t0 + i) * N + n] = s;
+      }
+    }
+    if (BC && tid < kCK && t0 + tid < L) {
+      float s = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kBwdWaves; ++w) s += s_ddt[w][tid];
+      p.ws_ddt[((int64_t)cb * p.Bt + b) * L + t0 + tid] = s;
     }
     if (more) commit(buf ^ 1, blk - 1);
     __syncthreads();
   }
 
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int n = n0 + j;
-    if (valid && n < N) p.ws_dA[(((int64_t)b * p.nseg + seg) * D + d) * N + n] = dAacc[j];
-  }
+  for (int j = 0; j < SPL; ++j)
+    if (valid && nj[j] < N) p.ws_dA[(((int64_t)b * p.nseg + seg) * D + d) * N + nj[j]] = dAacc[j];
   if (skip) {
-    // dD partial: the threads of one column accumulated disjoint rows
-    __shared__ float dred[RSTEP][kCh];
-    dred[srow0][scol] = dDacc;
+    // dD partial: the lanes of one channel accumulated disjoint steps
+    __shared__ float s_red[kBwdWaves * kWave];
+    s_red[tid] = dDacc;
     __syncthreads();
-    if (tid < kCh && svalid) {
-      float sacc = 0.0f;
+    if (tid < kBlkCh && cb * kBlkCh + tid < D) {
+      const int w = tid >> 3, cc = tid & 7;
+      float s = 0.0f;
 #pragma unroll
-      for (int r = 0; r < RSTEP; ++r) sacc += dred[r][tid];
-      p.ws_dD[((int64_t)b * p.nseg + seg) * D + sd] = sacc;
+      for (int k = 0; k < 8; ++k) s += s_red[w * kWave + cc + 8 * k];
+      p.ws_dD[((int64_t)b * p.nseg + seg) * D + cb * kBlkCh + tid] = s;
     }
   }
 }
@@ -1013,61 +1014,62 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_kerne
 // the right enters G.  It walks the segment forwards (P *= a, then G += P C dy),
 // so once every P of the workgroup is 0 (flushed at tile ends, flush_tiny) all
 // later steps add exact zeros and the walk stops there.
-template <int NG, bool EPI, typename T>
-__global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_agg_kernel(BwdArgs<T> p) {
-  constexpr int NS = NG * kSPW;
-  constexpr int NT = kWave * NG;
-  constexpr int RPT = kTT * kCh / NT;
-  constexpr int RSTEP = NT / kCh;
-  constexpr int BCE = kTT * NS / NT;
-  static_assert(BCE * NT == kTT * NS && RPT * NT == kTT * kCh, "staging must tile exactly");
+template <int SPL, bool EPI, typename T>
+__global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_agg_kernel(BwdArgs<T> p) {
+  constexpr int NS = 8 * SPL;
+  constexpr int NT = kWave * kBwdWaves;
+  constexpr int RPT = kTT * kBlkCh / NT;
+  constexpr int RSTEP = NT / kBlkCh;
+  constexpr int BCN = kTT * NS;
+  constexpr int BCE = (BCN + NT - 1) / NT;
+  constexpr int PF = SSM_BWD_PF;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int c = lane & (kCh - 1);
-  const int hf = lane >> 5;
+  const int c = lane & 7;
+  const int g = lane >> 3;
   const int b = blockIdx.y;
   const int cb = blockIdx.x;
   const int seg = blockIdx.z + 1;
   const int L = p.L, D = p.D, N = p.N;
   const int t_lo = seg * p.seg_len;
   const int t_hi = min(L, t_lo + p.seg_len);
-  const int d = cb * kCh + c;
+  const int cw = wave * 8 + c;
+  const int d = cb * kBlkCh + cw;
   const bool valid = d < D;
   const int dc = valid ? d : 0;
-  const int n0 = wave * kSPW + 2 * hf;
   const bool rev = p.flags & SSM_REVERSE;
   const bool comp = rev && (p.flags & SSM_COMPLEMENT);
   const bool gate = EPI && (p.flags & SSM_GATE);
   const bool dsp = p.flags & SSM_DELTA_SOFTPLUS;
-  const int scol = tid & (kCh - 1);
-  const int srow0 = tid / kCh;
-  const int sd = cb * kCh + scol;
+  const int scol = tid & (kBlkCh - 1);
+  const int srow0 = tid / kBlkCh;
+  const int sd = cb * kBlkCh + scol;
   const bool svalid = sd < D;
   const int sdc = svalid ? sd : 0;
   const int sq = comp ? D - 1 - sdc : sdc;
 
-  float A2[2], G[2] = {0.0f, 0.0f}, P[2] = {1.0f, 1.0f};
-  bool live[2];
+  float A2[SPL], G[SPL], P[SPL];
+  bool live[SPL];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    live[j] = valid && n0 + j < N;
-    A2[j] = live[j] ? p.A[(int64_t)dc * N + n0 + j] * kLog2e : 0.0f;
+  for (int j = 0; j < SPL; ++j) {
+    live[j] = valid && SPL * g + j < N;
+    A2[j] = live[j] ? p.A[dc * N + SPL * g + j] * kLog2e : 0.0f;
+    G[j] = 0.0f;
+    P[j] = 1.0f;
   }
 
-  __shared__ float s_dt[2][kTT][kCh], s_dy[2][kTT][kCh];
+  __shared__ float2 s_dy[2][kTT][kBlkCh];  // (delta, dy of the scan)
   __shared__ __attribute__((aligned(16))) float s_C[2][kTT][NS];
-  __shared__ int s_alive[2][NG];
+  __shared__ int s_alive[2][kBwdWaves];
 
-  const int64_t bLD = (int64_t)b * L * D;
-  const int64_t bLN = (int64_t)b * L * N;
   const int dtD = p.dstride ? D : 1;
   const int scol_dt = p.dstride ? sdc : 0;
   const T* __restrict__ dt_b = p.delta + (int64_t)b * L * dtD;
   const int ldy = p.ldy, ldz = p.ldz;
   const T* __restrict__ dy_b = p.dy + (int64_t)b * L * ldy;
   const T* __restrict__ z_b = EPI ? p.z + (int64_t)b * L * ldz : nullptr;
-  const T* __restrict__ C_b = p.Cc + bLN;
+  const T* __restrict__ C_b = p.Cc + (int64_t)b * L * N;
   const int LN = L * N;
 
   float r_dt[RPT], r_dy[RPT], r_gz[RPT], r_C[BCE];
@@ -1083,44 +1085,32 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_agg_k
 #pragma unroll
     for (int k = 0; k < BCE; ++k) {
       const int e = tid + k * NT;
-      int gi;
-      if (NS == N) {
-        gi = t0 * N + e;
-      } else {
-        const int i = e / NS, n = e - i * NS;
-        gi = (t0 + i) * N + min(n, N - 1);
+      if (BCN % NT == 0 || e < BCN) {
+        const int i = e / NS, n = e - (e / NS) * NS;
+        r_C[k] = ld32(C_b, (uint32_t)min((t0 + i) * N + min(n, N - 1), LN - 1));
       }
-      r_C[k] = ld32(C_b, (uint32_t)min(gi, LN - 1));
-    }
-  };
-  auto stage_dt = [&](int buf, int t0, auto sp_tag) {
-#pragma unroll
-    for (int k = 0; k < RPT; ++k) {
-      const int i = srow0 + k * RSTEP;
-      const bool in = svalid && t0 + i < L;
-      const float v = decltype(sp_tag)::value ? softplus(r_dt[k]) : r_dt[k];
-      s_dt[buf][i][scol] = in ? v : 0.0f;
     }
   };
   auto commit = [&](int buf, int t0) {
-    if (dsp) stage_dt(buf, t0, std::true_type{}); else stage_dt(buf, t0, std::false_type{});
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
       const int i = srow0 + k * RSTEP;
       const bool in = svalid && t0 + i < L;
-      const float go = in ? r_dy[k] : 0.0f;
+      const float dtv = dsp ? softplus(r_dt[k]) : r_dt[k];
+      float go = in ? r_dy[k] : 0.0f;
       if (gate) {
         const float gz = in ? r_gz[k] : 0.0f;
-        s_dy[buf][i][scol] = go * gz * sigmoid(gz);  // as the main backward pass stages it
-      } else {
-        s_dy[buf][i][scol] = go;
+        go *= gz * sigmoid(gz);  // as the main backward pass stages it
       }
+      s_dy[buf][i][scol] = in ? make_float2(dtv, go) : make_float2(0.0f, 0.0f);
     }
 #pragma unroll
     for (int k = 0; k < BCE; ++k) {
       const int e = tid + k * NT;
-      const int i = e / NS, n = e - (e / NS) * NS;
-      (&s_C[buf][0][0])[e] = (t0 + i < L && n < N) ? r_C[k] : 0.0f;
+      if (BCN % NT == 0 || e < BCN) {
+        const int i = e / NS, n = e - (e / NS) * NS;
+        (&s_C[buf][0][0])[e] = (t0 + i < L && n < N) ? r_C[k] : 0.0f;
+      }
     }
   };
 
@@ -1131,41 +1121,40 @@ __global__ void __launch_bounds__(kWave* NG, NG <= 4 ? 8 / NG : 1) ssm_bwd_agg_k
   for (int t0 = t_lo;; t0 += kTT, buf ^= 1) {
     const bool more = t0 + kTT < t_hi;
     if (more) fetch(t0 + kTT);
-    const int tn = min(kTT, L - t0);
-    auto tile = [&](auto full_tag) {
-      constexpr bool kFull = decltype(full_tag)::value;
-      float dd[kTT], dyv[kTT];
-#pragma unroll
-      for (int i = 0; i < kTT; ++i) {
-        if (kFull || i < tn) {
-          dd[i] = s_dt[buf][i][c];
-          dyv[i] = s_dy[buf][i][c];
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < kTT; ++i) {
-        if (kFull || i < tn) {
-          const float2 Cv = *reinterpret_cast<const float2*>(&s_C[buf][i][n0]);
-          P[0] *= fast_exp2(A2[0] * dd[i]);
-          P[1] *= fast_exp2(A2[1] * dd[i]);
-          G[0] = fmaf(P[0], Cv.x * dyv[i], G[0]);
-          G[1] = fmaf(P[1], Cv.y * dyv[i], G[1]);
-        }
-      }
+    constexpr int R = PF + 1;
+    float2 xd[R];
+    float Cq[R][SPL];
+    auto pre = [&](int i) {
+      xd[i % R] = s_dy[buf][i][cw];
+      lds_vec<SPL>(&s_C[buf][i][SPL * g], Cq[i % R]);
     };
-    if (tn == kTT) tile(std::true_type{}); else tile(std::false_type{});
+#pragma unroll
+    for (int i = 0; i < PF; ++i) pre(i);
+#pragma unroll
+    for (int i = 0; i < kTT; ++i) {
+      if (i + PF < kTT) pre(i + PF);
+      __builtin_amdgcn_sched_barrier(0);
+      const float dd = xd[i % R].x, dyv = xd[i % R].y;
+#pragma unroll
+      for (int j = 0; j < SPL; ++j) {
+        P[j] *= fast_exp2(A2[j] * dd);
+        G[j] = fmaf(P[j], Cq[i % R][j] * dyv, G[j]);
+      }
+    }
     if (more) commit(buf ^ 1, t0 + kTT);
     // as in the forward aggregate: flushed products end the walk
     flush_tiny(P);
-    const bool alive = (live[0] && P[0] != 0.0f) || (live[1] && P[1] != 0.0f);
-    if (!barrier_any<NG>(alive, s_alive[buf]) || !more) break;
+    bool alive = false;
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) alive = alive || (live[j] && P[j] != 0.0f);
+    if (!barrier_any<kBwdWaves>(alive, s_alive[buf]) || !more) break;
   }
   const int64_t o = (int64_t)b * p.nseg + seg;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < SPL; ++j) {
     if (live[j]) {
-      p.agg_G[(o * N + n0 + j) * D + d] = G[j];
-      p.agg_P[(o * N + n0 + j) * D + d] = P[j];
+      p.agg_G[(o * N + SPL * g + j) * D + d] = G[j];
+      p.agg_P[(o * N + SPL * g + j) * D + d] = P[j];
     }
   }
 }
@@ -1211,18 +1200,18 @@ __global__ void reduce_parts_kernel(const float* __restrict__ ws, TO* __restrict
 // ------------------------------------------------------------------- host side
 
 struct Shape {
-  int B, L, D, N, nblk, ncb;
-  int NG;    // waves per workgroup (4 states each)
-  bool epi;  // skip / gate epilogue fused
-  int seg_len, nseg;  // time segments per row
-  int ldy, ldz;       // row strides of y / dy and of z
+  int B, L, D, N, nblk, ncb;  // ncb: 64-channel blocks
+  int spl_f, spl_b;           // states per lane of the forward and backward kernels
+  bool epi;                   // skip / gate epilogue fused
+  int seg_len, nseg;          // time segments per row
+  int ldy, ldz;               // row strides of y / dy and of z
 };
 
-// Automatic time split: a row is split only when the unsplit grid would leave
-// more than half of the resident-wave slots empty (256 CUs x 4 SIMDs x 2 waves
-// of these kernels on MI355X), into enough segments to fill them, each at
-// least kMinAutoSeg steps long.  The choice depends on the desc alone, so a
-// given desc always computes in the same order.
+// Automatic time split: a row is split only when the unsplit backward grid
+// would leave more than half of the resident-wave slots empty (256 CUs x 4
+// SIMDs x 2 waves on MI355X), into enough segments to fill them, each at least
+// kMinAutoSeg steps long.  The choice depends on the desc alone, so a given
+// desc always computes in the same order.
 constexpr int kFillWaves = 2048;
 constexpr int kMinAutoSeg = 512;
 constexpr int kMaxSeg = 1024;
@@ -1230,7 +1219,7 @@ constexpr int kMaxSeg = 1024;
 void choose_segments(const ssm_desc_t* desc, Shape* s) {
   int64_t want = desc->segments;
   if (want == 0) {
-    const int64_t waves = (int64_t)s->B * s->ncb * s->NG;
+    const int64_t waves = (int64_t)s->B * s->ncb * kBwdWaves;
     want = 2 * waves >= kFillWaves ? 1 : (kFillWaves + waves - 1) / waves;
     want = std::min<int64_t>(want, std::max(1, s->L / kMinAutoSeg));
   }
@@ -1268,32 +1257,31 @@ int validate(const ssm_desc_t* desc, Shape* s) {
   s->L = (int)desc->seqlen;
   s->D = (int)desc->dim;
   s->N = (int)desc->dstate;
-  s->ncb = (s->D + kCh - 1) / kCh;
+  s->ncb = (s->D + kBlkCh - 1) / kBlkCh;
   s->ldy = desc->ld_y ? (int)desc->ld_y : s->D;
   s->ldz = desc->ld_z ? (int)desc->ld_z : s->D;
   s->nblk = (s->L + kCK - 1) / kCK;
   // extra epilogue staging: the gate, and the reverse skip's u at the mirrored position
   s->epi = (desc->flags & SSM_GATE) || ((desc->flags & SSM_SKIP) && (desc->flags & SSM_REVERSE));
-  const int ng = (s->N + kSPW - 1) / kSPW;
-  s->NG = 1;
-  while (s->NG < ng) s->NG *= 2;  // instantiated wave counts: 1, 2, 4, 8
+  s->spl_f = s->N <= 16 ? 4 : 8;  // 4 state rows per forward wave
+  s->spl_b = s->N <= 16 ? 2 : 4;  // 8 state groups per backward wave
   choose_segments(desc, s);
   return SSM_OK;
 }
 
-template <int G, bool E, typename F>
-bool dispatch_one(const Shape& s, F&& f) {
-  if (s.NG != G || s.epi != E) return false;
-  f(std::integral_constant<int, G>{}, std::integral_constant<bool, E>{});
-  return true;
-}
-
-// Calls f(ng, epi) with the compile-time variant matching s.
-template <typename F>
-bool dispatch_variant(const Shape& s, F&& f) {
-  return dispatch_one<1, false>(s, f) || dispatch_one<2, false>(s, f) || dispatch_one<4, false>(s, f) ||
-         dispatch_one<8, false>(s, f) || dispatch_one<1, true>(s, f) || dispatch_one<2, true>(s, f) ||
-         dispatch_one<4, true>(s, f) || dispatch_one<8, true>(s, f);
+// Calls f(spl, epi) with the compile-time variant matching s (spl = s.spl_f
+// for the forward kernels, s.spl_b for the backward ones).
+template <int S0, int S1, typename F>
+bool dispatch_spl(int spl, bool epi, F&& f) {
+  auto one = [&](auto sv, auto ev) {
+    if (spl != decltype(sv)::value || epi != decltype(ev)::value) return false;
+    f(sv, ev);
+    return true;
+  };
+  return one(std::integral_constant<int, S0>{}, std::false_type{}) ||
+         one(std::integral_constant<int, S1>{}, std::false_type{}) ||
+         one(std::integral_constant<int, S0>{}, std::true_type{}) ||
+         one(std::integral_constant<int, S1>{}, std::true_type{});
 }
 
 size_t ckpt_floats(const Shape& s) { return (size_t)s.B * s.nblk * s.N * s.D; }
@@ -1346,17 +1334,23 @@ int launch_fwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const voi
   a.ldy = s.ldy;
   a.ldz = s.ldz;
   a.dstride = desc->delta_broadcast ? 0 : 1;
+  const bool vec = s.D % 4 == 0 && !desc->delta_broadcast && reinterpret_cast<uintptr_t>(u) % (4 * sizeof(T)) == 0 &&
+                   reinterpret_cast<uintptr_t>(delta) % (4 * sizeof(T)) == 0;
   a.flags = desc->flags;
-  if (!dispatch_variant(s, [&](auto ng, auto epi) {
-        constexpr int G = decltype(ng)::value;
+  if (!dispatch_spl<4, 8>(s.spl_f, s.epi, [&](auto spl, auto epi) {
+        constexpr int S = decltype(spl)::value;
         constexpr bool E = decltype(epi)::value;
         auto go = [&](auto sp) {
           constexpr bool SP = decltype(sp)::value;
           if (s.nseg > 1)  // aggregates of every segment but the last
-            hipLaunchKernelGGL((ssm_fwd_agg_kernel<G, SP, T>), dim3(s.ncb, s.B, s.nseg - 1), dim3(kWave * G), 0,
-                               st, a);
-          hipLaunchKernelGGL((ssm_fwd_kernel<G, E, SP, T>), dim3(s.ncb, s.B, s.nseg), dim3(kWave * G), 0,
-                             st, a);
+            hipLaunchKernelGGL((ssm_fwd_agg_kernel<S, SP, T>), dim3(s.ncb, s.B, s.nseg - 1),
+                               dim3(kWave * kFwdWaves), 0, st, a);
+          if (vec)
+            hipLaunchKernelGGL((ssm_fwd_kernel<S, E, SP, true, T>), dim3(s.ncb, s.B, s.nseg),
+                               dim3(kWave * kFwdWaves), 0, st, a);
+          else
+            hipLaunchKernelGGL((ssm_fwd_kernel<S, E, SP, false, T>), dim3(s.ncb, s.B, s.nseg),
+                               dim3(kWave * kFwdWaves), 0, st, a);
         };
         if (desc->flags & SSM_DELTA_SOFTPLUS) go(std::true_type{}); else go(std::false_type{});
       }))
@@ -1404,12 +1398,18 @@ int launch_bwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const voi
   a.ldz = s.ldz;
   a.dstride = bcast ? 0 : 1;
   a.flags = desc->flags;
-  if (!dispatch_variant(s, [&](auto ng, auto epi) {
-        constexpr int G = decltype(ng)::value;
+  if (!dispatch_spl<2, 4>(s.spl_b, s.epi, [&](auto spl, auto epi) {
+        constexpr int S = decltype(spl)::value;
         constexpr bool E = decltype(epi)::value;
         if (s.nseg > 1)  // adjoint aggregates of every segment but the first
-          hipLaunchKernelGGL((ssm_bwd_agg_kernel<G, E, T>), dim3(s.ncb, s.B, s.nseg - 1), dim3(kWave * G), 0, st, a);
-        hipLaunchKernelGGL((ssm_bwd_kernel<G, E, T>), dim3(s.ncb, s.B, s.nseg), dim3(kWave * G), 0, st, a);
+          hipLaunchKernelGGL((ssm_bwd_agg_kernel<S, E, T>), dim3(s.ncb, s.B, s.nseg - 1), dim3(kWave * kBwdWaves),
+                             0, st, a);
+        if (desc->delta_broadcast)
+          hipLaunchKernelGGL((ssm_bwd_kernel<S, E, true, T>), dim3(s.ncb, s.B, s.nseg), dim3(kWave * kBwdWaves), 0,
+                             st, a);
+        else
+          hipLaunchKernelGGL((ssm_bwd_kernel<S, E, false, T>), dim3(s.ncb, s.B, s.nseg), dim3(kWave * kBwdWaves), 0,
+                             st, a);
       }))
     return fail(SSM_ERR_UNSUPPORTED, "no kernel variant for this shape");
   int rc = hip_check(hipGetLastError(), "ssm_bwd launch");
