@@ -341,29 +341,39 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
     auto tile = [&](auto full_tag, auto ck_tag) {
       constexpr bool kFull = decltype(full_tag)::value;
       constexpr bool kCkpt = decltype(ck_tag)::value;
-      // operands of steps i .. i + PF in a ring of PF + 1 register sets
-      constexpr int R = PF + 1;
+      // operands of steps i .. i + PF + 1 in a ring of PF + 2 register sets;
+      // (u, delta) of two steps are read by one LDS instruction
+      static_assert(PF % 2 == 0, "operands are prefetched in step pairs");
+      constexpr int R = PF + 2;
       float2 ud[R];
       float Bq[R][SPL], Cq[R][SPL];
-      auto pre = [&](int i) {
+      auto pre = [&](int i) {  // steps i, i + 1 (i even)
         ud[i % R] = s_ud[buf][i][cw];
-        lds_vec<SPL>(&s_B[buf][i][SPL * g], Bq[i % R]);
-        lds_vec<SPL>(&s_C[buf][i][SPL * g], Cq[i % R]);
+        ud[(i + 1) % R] = s_ud[buf][i + 1][cw];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          lds_vec<SPL>(&s_B[buf][i + k][SPL * g], Bq[(i + k) % R]);
+          lds_vec<SPL>(&s_C[buf][i + k][SPL * g], Cq[(i + k) % R]);
+        }
       };
 #pragma unroll
-      for (int i = 0; i < PF; ++i) pre(i);
+      for (int i = 0; i < PF; i += 2) pre(i);
       float yp[4];
+      // running row offsets of the y and checkpoint stores (scalars)
+      uint32_t yro = (uint32_t)(rev ? L - 4 - t0 : t0) * yrowb;
+      const uint32_t ystep = rev ? 0u - 4u * yrowb : 4u * yrowb;
+      uint32_t cro = (uint32_t)(t0 / kCK) * ckrowb;
 #pragma unroll
       for (int i = 0; i < kTT; ++i) {
-        if (i + PF < kTT) pre(i + PF);
+        if (i % 2 == 0 && i + PF < kTT) pre(i + PF);
         __builtin_amdgcn_sched_barrier(0);
         if (kCkpt && (i % kCK) == 0 && (kFull || t0 + i < L)) {
-          const uint32_t ro = (uint32_t)((t0 + i) / kCK) * ckrowb;
 #pragma unroll
           for (int j = 0; j < SPL; ++j) {
             const int n = SPL * g + j;
-            if (kFull || (valid && n < N)) bst<float>(rck, cko[j], ro, h[j]);
+            if (kFull || (valid && n < N)) bst<float>(rck, cko[j], cro, h[j]);
           }
+          cro += ckrowb;
         }
         const float uu = ud[i % R].x, dd = ud[i % R].y;
         const float w = dd * uu;
@@ -392,8 +402,9 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
             yv *= zz * sigmoid(zz);
           }
           if constexpr (kFull) {
-            // the uniform row L-1-(t0+i) is >= 0 on a full tile
-            bst<T>(ry, yo, (uint32_t)(rev ? L - 1 - t0 - i : t0 + i - 3) * yrowb, yv);
+            // row t0+i-3 (or L-1-(t0+i) >= 0 with the reverse map) plus the lane's yo
+            bst<T>(ry, yo, yro, yv);
+            yro += ystep;
           } else if (valid && t < L) {
             bst<T>(ry, (uint32_t)(rev ? L - 1 - t : t) * yrowb + (uint32_t)(q * sizeof(T)), 0, yv);
           }
