@@ -60,13 +60,21 @@ constexpr int kWave = 64;
 constexpr int kBlkCh = 64;    // channels per workgroup
 constexpr int kFwdWaves = 4;  // forward: 16 channels x 4 state rows per wave
 constexpr int kBwdWaves = 8;  // backward: 8 channels x 8 state groups per wave
-constexpr int kTT = 32;       // forward time tile
+#ifndef SSM_FWD_TT
+#define SSM_FWD_TT 32
+#endif
+constexpr int kTT = SSM_FWD_TT;  // forward time tile
 constexpr int kCK = 16;       // checkpoint interval = backward block length
 #ifndef SSM_FWD_PF
 #define SSM_FWD_PF 2
 #endif
 #ifndef SSM_BWD_PF
 #define SSM_BWD_PF 1
+#endif
+// backward: the channel sums of step i are issued with step i + 1's compute,
+// so their dependent DPP chains interleave with independent work
+#ifndef SSM_BWD_PIPE
+#define SSM_BWD_PIPE 1
 #endif
 
 // S consecutive floats of LDS (16-byte aligned when S >= 4) into registers
@@ -235,8 +243,9 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
   // u and delta as 4-element vectors: thread -> rows vr, vr + 16, channels
   // vc .. vc + 3 (D % 4 == 0, so a vector is wholly inside or outside D).
   float r_u[RPT], r_dt[RPT], r_eu[RPT], r_ez[RPT], r_B[BCE], r_C[BCE];
-  float4 v_u[2], v_dt[2];
-  static_assert(RPT == 8 && NT == 256, "vector staging covers 2 rows of 4 channels per thread");
+  constexpr int VK = kTT / 16;  // vector rows per thread
+  float4 v_u[VK], v_dt[VK];
+  static_assert(NT == 256 && kTT % 16 == 0, "vector staging: 16 threads per row, 16 rows per pass");
   const int vr = tid >> 4, vc = (tid & 15) * 4;
   const bool vin = cb * kBlkCh + vc < D;
   const uint32_t vcb = (uint32_t)((vin ? cb * kBlkCh + vc : 0) * sizeof(T));
@@ -244,7 +253,7 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
   auto fetch = [&](int t0) {
     if constexpr (VEC) {
 #pragma unroll
-      for (int k = 0; k < 2; ++k) {
+      for (int k = 0; k < VK; ++k) {
         const uint32_t o = (uint32_t)min(t0 + vr + 16 * k, L - 1) * rowb + vcb;
         v_u[k] = bld4<T>(ru, o, 0);
         v_dt[k] = bld4<T>(rdt, o, 0);
@@ -280,7 +289,7 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
   auto commit = [&](int buf, int t0) {
     if constexpr (VEC) {
 #pragma unroll
-      for (int k = 0; k < 2; ++k) {
+      for (int k = 0; k < VK; ++k) {
         const bool in = vin && t0 + vr + 16 * k < L;
         const float4 uv = v_u[k], dr = v_dt[k];
         const float4 dv = SP ? make_float4(softplus(dr.x), softplus(dr.y), softplus(dr.z), softplus(dr.w)) : dr;
@@ -858,6 +867,7 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
 #pragma unroll
       for (int i = 0; i < PF; ++i) pre(i);
       float yp[4];
+      float vCp[SPL], vBp[SPL];  // (SSM_BWD_PIPE) the previous step's products
 #pragma unroll
       for (int i = 0; i < kCK; ++i) {
         if (i + PF < kCK) pre(i + PF);
@@ -873,7 +883,14 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
           h[j] = fmaf(a, h[j], bc[i % R][j] * w);
           vC[j] = dyv * h[j];
         }
-        s_dC[wave][i][SPL * g + sig] = chan_reduce8<SPL>(vC);
+        if constexpr (SSM_BWD_PIPE) {
+          if (i > 0) s_dC[wave][i - 1][SPL * g + sig] = chan_reduce8<SPL>(vCp);
+#pragma unroll
+          for (int j = 0; j < SPL; ++j) vCp[j] = vC[j];
+          if (i == kCK - 1) s_dC[wave][i][SPL * g + sig] = chan_reduce8<SPL>(vCp);
+        } else {
+          s_dC[wave][i][SPL * g + sig] = chan_reduce8<SPL>(vC);
+        }
         if (gate) {
           float ys = bc[i % R][SPL] * h[0];
 #pragma unroll
@@ -919,7 +936,14 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
           vB[j] = f * w;
           gc[j] = gg;
         }
-        s_dB[wave][i][SPL * g + sig] = chan_reduce8<SPL>(vB);
+        if constexpr (SSM_BWD_PIPE) {
+          if (i < kCK - 1) s_dB[wave][i + 1][SPL * g + sig] = chan_reduce8<SPL>(vBp);
+#pragma unroll
+          for (int j = 0; j < SPL; ++j) vBp[j] = vB[j];
+          if (i == 0) s_dB[wave][0][SPL * g + sig] = chan_reduce8<SPL>(vBp);
+        } else {
+          s_dB[wave][i][SPL * g + sig] = chan_reduce8<SPL>(vB);
+        }
         // du = delta sum_n f B; ddelta = sum_n f (A a h_{t-1} + B u)
         const float v1 = dd * s1, v2 = fmaf(uu, s1, s2);
         if (i & 1) {
