@@ -461,7 +461,7 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_agg_kernel(FwdArg
   const bool valid = d < D;
   const int dc = valid ? d : 0;
   const int scol = tid & (kBlkCh - 1);
-  const int srow0 = tid / kBlkCh;
+  const int srow0 = wave;  // = tid / kBlkCh: the staged rows of a wave are uniform
   const int sd = cb * kBlkCh + scol;
   const bool svalid = sd < D;
   const int sdc = svalid ? sd : 0;
@@ -486,21 +486,24 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_agg_kernel(FwdArg
   const T* __restrict__ dt_b = p.delta + (int64_t)b * L * dtD;
   const T* __restrict__ B_b = p.Bc + (int64_t)b * L * N;
   const int LN = L * N;
+  const buf_t ru = make_buf(u_b), rdt = make_buf(dt_b), rB = make_buf(B_b);
+  const uint32_t so_c = (uint32_t)(sdc * sizeof(T)), so_dt = (uint32_t)(scol_dt * sizeof(T));
+  const uint32_t rowb = (uint32_t)(D * sizeof(T)), dtrowb = (uint32_t)(dtD * sizeof(T));
 
   float r_u[RPT], r_dt[RPT], r_B[BCE];
   auto fetch = [&](int t0) {
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
-      const int tc = min(t0 + srow0 + k * RSTEP, L - 1);
-      r_u[k] = ld32(u_b, (uint32_t)(tc * D + sdc));
-      r_dt[k] = ld32(dt_b, (uint32_t)(tc * dtD + scol_dt));
+      const int tc = min(t0 + srow0 + k * RSTEP, L - 1);  // wave-uniform
+      r_u[k] = bld<T>(ru, so_c, (uint32_t)tc * rowb);
+      r_dt[k] = bld<T>(rdt, so_dt, (uint32_t)tc * dtrowb);
     }
 #pragma unroll
     for (int k = 0; k < BCE; ++k) {
       const int e = tid + k * NT;
       if (BCN % NT == 0 || e < BCN) {
         const int i = e / NS, n = e - (e / NS) * NS;
-        r_B[k] = ld32(B_b, (uint32_t)min((t0 + i) * N + min(n, N - 1), LN - 1));
+        r_B[k] = bld<T>(rB, (uint32_t)(min((t0 + i) * N + min(n, N - 1), LN - 1) * sizeof(T)), 0);
       }
     }
   };
@@ -1078,7 +1081,7 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_agg_kernel(BwdArg
   const bool gate = EPI && (p.flags & SSM_GATE);
   const bool dsp = p.flags & SSM_DELTA_SOFTPLUS;
   const int scol = tid & (kBlkCh - 1);
-  const int srow0 = tid / kBlkCh;
+  const int srow0 = wave;  // = tid / kBlkCh: the staged rows of a wave are uniform
   const int sd = cb * kBlkCh + scol;
   const bool svalid = sd < D;
   const int sdc = svalid ? sd : 0;
@@ -1107,22 +1110,26 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_agg_kernel(BwdArg
   const T* __restrict__ C_b = p.Cc + (int64_t)b * L * N;
   const int LN = L * N;
 
+  const buf_t rdt = make_buf(dt_b), rdy = make_buf(dy_b), rz = make_buf(EPI ? z_b : dy_b), rC = make_buf(C_b);
+  const uint32_t so_dt = (uint32_t)(scol_dt * sizeof(T)), so_q = (uint32_t)(sq * sizeof(T));
+  const uint32_t dtrowb = (uint32_t)(dtD * sizeof(T)), dyrowb = (uint32_t)(ldy * sizeof(T));
+  const uint32_t zrowb = (uint32_t)(ldz * sizeof(T));
   float r_dt[RPT], r_dy[RPT], r_gz[RPT], r_C[BCE];
   auto fetch = [&](int t0) {
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
-      const int tc = min(t0 + srow0 + k * RSTEP, L - 1);
+      const int tc = min(t0 + srow0 + k * RSTEP, L - 1);  // wave-uniform
       const int pr = rev ? L - 1 - tc : tc;
-      r_dt[k] = ld32(dt_b, (uint32_t)(tc * dtD + scol_dt));
-      r_dy[k] = ld32(dy_b, (uint32_t)(pr * ldy + sq));
-      if (gate) r_gz[k] = ld32(z_b, (uint32_t)(pr * ldz + sq));
+      r_dt[k] = bld<T>(rdt, so_dt, (uint32_t)tc * dtrowb);
+      r_dy[k] = bld<T>(rdy, so_q, (uint32_t)pr * dyrowb);
+      if (gate) r_gz[k] = bld<T>(rz, so_q, (uint32_t)pr * zrowb);
     }
 #pragma unroll
     for (int k = 0; k < BCE; ++k) {
       const int e = tid + k * NT;
       if (BCN % NT == 0 || e < BCN) {
         const int i = e / NS, n = e - (e / NS) * NS;
-        r_C[k] = ld32(C_b, (uint32_t)min((t0 + i) * N + min(n, N - 1), LN - 1));
+        r_C[k] = bld<T>(rC, (uint32_t)(min((t0 + i) * N + min(n, N - 1), LN - 1) * sizeof(T)), 0);
       }
     }
   };
