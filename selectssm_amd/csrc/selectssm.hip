@@ -64,7 +64,10 @@ constexpr int kBwdWaves = 8;  // backward: 8 channels x 8 state groups per wave
 #define SSM_FWD_TT 32
 #endif
 constexpr int kTT = SSM_FWD_TT;  // forward time tile
-constexpr int kCK = 16;       // checkpoint interval = backward block length
+#ifndef SSM_CK
+#define SSM_CK 16
+#endif
+constexpr int kCK = SSM_CK;   // checkpoint interval = backward block length
 #ifndef SSM_FWD_PF
 #define SSM_FWD_PF 2
 #endif
@@ -368,6 +371,9 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
 #pragma unroll
       for (int i = 0; i < PF; i += 2) pre(i);
       float yp[4];
+      // epilogue operands of the current 4-step group at this lane's output
+      // step, read at the group's first step so their LDS latency is covered
+      float uo = 0.0f, zo = 0.0f;
       // running row offsets of the y and checkpoint stores (scalars)
       uint32_t yro = (uint32_t)(rev ? L - 4 - t0 : t0) * yrowb;
       const uint32_t ystep = rev ? 0u - 4u * yrowb : 4u * yrowb;
@@ -375,6 +381,16 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
 #pragma unroll
       for (int i = 0; i < kTT; ++i) {
         if (i % 2 == 0 && i + PF < kTT) pre(i + PF);
+        if ((i & 3) == 0) {
+          // skip (Dq is 0 without it): u at the output position, which the
+          // reverse map makes another element (staged in EPI builds)
+          const int ti = i + yoff;
+          uo = s_ud[buf][ti][cw].x;
+          if constexpr (EPI) {
+            if (stage_eu) uo = s_eu[buf][ti][cw];
+            if (gate) zo = s_ez[buf][ti][cw];
+          }
+        }
         __builtin_amdgcn_sched_barrier(0);
         if (kCkpt && (i % kCK) == 0 && (kFull || t0 + i < L)) {
 #pragma unroll
@@ -399,17 +415,8 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
           float yv = rows_transpose_sum4(yp[0], yp[1], yp[2], yp[3]);
           const int ti = i - 3 + yoff;
           const int t = t0 + ti;
-          // skip (Dq is 0 without it): u at the output position, which the
-          // reverse map makes another element (staged in EPI builds)
-          float uo = s_ud[buf][ti][cw].x;
-          if constexpr (EPI) {
-            if (stage_eu) uo = s_eu[buf][ti][cw];
-          }
           yv = fmaf(uo, Dq, yv);
-          if (gate) {
-            const float zz = s_ez[buf][ti][cw];
-            yv *= zz * sigmoid(zz);
-          }
+          if (gate) yv *= zo * sigmoid(zo);
           if constexpr (kFull) {
             // row t0+i-3 (or L-1-(t0+i) >= 0 with the reverse map) plus the lane's yo
             bst<T>(ry, yo, yro, yv);
@@ -871,9 +878,18 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
       for (int i = 0; i < PF; ++i) pre(i);
       float yp[4];
       float vCp[SPL], vBp[SPL];  // (SSM_BWD_PIPE) the previous step's products
+      // gate: operands of the current 4-step group at this lane's output
+      // step, read at the group's first step
+      float ge_u = 0.0f, ge_z = 0.0f, ge_o = 0.0f;
 #pragma unroll
       for (int i = 0; i < kCK; ++i) {
         if (i + PF < kCK) pre(i + PF);
+        if (gate && (i & 3) == 0) {
+          const int ti = i + yrow_step(orow);
+          if (skip) ge_u = stage_eu ? s_eu[buf][ti][cw] : s_x[buf][ti][cw].x;
+          ge_z = s_gz[buf][ti][cw];
+          ge_o = s_go[buf][ti][cw];
+        }
         __builtin_amdgcn_sched_barrier(0);
         const float uu = xr[i % R].x, dd = xr[i % R].y, dyv = xr[i % R].z;
         const float w = dd * uu;
@@ -904,10 +920,10 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
             yv += dpp_mov<kDppRor8>(yv);
             const int ti = i - 3 + yrow_step(orow);
             const int t = t0 + ti;
-            if (skip) yv = fmaf(stage_eu ? s_eu[buf][ti][cw] : s_x[buf][ti][cw].x, Dq, yv);
-            const float zz = s_gz[buf][ti][cw];
+            if (skip) yv = fmaf(ge_u, Dq, yv);
+            const float zz = ge_z;
             const float sg = sigmoid(zz);
-            const float dzv = s_go[buf][ti][cw] * yv * sg * (1.0f + zz * (1.0f - sg));
+            const float dzv = ge_o * yv * sg * (1.0f + zz * (1.0f - sg));
             // both halves of the row hold the value; both store it
             if constexpr (kFull) {
               bst<T>(rdz, dzo, (uint32_t)(rev ? L - 1 - t0 - i : t0 + i - 3) * rowb, dzv);
