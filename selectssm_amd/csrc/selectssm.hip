@@ -385,10 +385,13 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
           // skip (Dq is 0 without it): u at the output position, which the
           // reverse map makes another element (staged in EPI builds)
           const int ti = i + yoff;
-          uo = s_ud[buf][ti][cw].x;
           if constexpr (EPI) {
-            if (stage_eu) uo = s_eu[buf][ti][cw];
-            if (gate) zo = s_ez[buf][ti][cw];
+            // branch-free: one read from either array; z is read (and
+            // discarded below) without the gate as well
+            uo = *(stage_eu ? &s_eu[buf][ti][cw] : &s_ud[buf][ti][cw].x);
+            zo = s_ez[buf][ti][cw];
+          } else {
+            uo = s_ud[buf][ti][cw].x;
           }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -410,13 +413,18 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
           ys = j == 0 ? Cq[i % R][0] * h[0] : fmaf(Cq[i % R][j], h[j], ys);
         }
         yp[i & 3] = ys;
+        if constexpr (EPI) {
+          // the gate factor z sigmoid(z) (1 without the gate), two steps
+          // after its read and ahead of its use
+          if ((i & 3) == 2) zo = gate ? zo * sigmoid(zo) : 1.0f;
+        }
         if ((i & 3) == 3) {
           // y of steps i-3..i summed over the state rows: this lane's row holds step ti
           float yv = rows_transpose_sum4(yp[0], yp[1], yp[2], yp[3]);
           const int ti = i - 3 + yoff;
           const int t = t0 + ti;
           yv = fmaf(uo, Dq, yv);
-          if (gate) yv *= zo * sigmoid(zo);
+          if constexpr (EPI) yv *= zo;
           if constexpr (kFull) {
             // row t0+i-3 (or L-1-(t0+i) >= 0 with the reverse map) plus the lane's yo
             bst<T>(ry, yo, yro, yv);
