@@ -52,16 +52,11 @@ __device__ __forceinline__ void st<float>(float* p, int64_t i, float v) {
 }
 template <>
 __device__ __forceinline__ void st<bf16>(bf16* p, int64_t i, float v) {
-  // round to nearest even; NaN stays a quiet NaN
-  uint32_t x = __float_as_uint(v);
-  uint16_t r;
-  if ((x & 0x7fffffffu) > 0x7f800000u) {
-    r = static_cast<uint16_t>((x >> 16) | 0x40u);
-  } else {
-    x += 0x7fffu + ((x >> 16) & 1u);
-    r = static_cast<uint16_t>(x >> 16);
-  }
-  p[i].bits = r;
+  // one v_cvt_pk_bf16_f32: round to nearest even, denormals kept, NaN stays a
+  // quiet NaN.  Checked on gfx950 against the integer form of that rounding
+  // (x + 0x7fff + bit 16, NaN -> x >> 16 | 0x40) for all 2^32 inputs: equal
+  // apart from NaN payloads.
+  p[i].bits = __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
 }
 
 // store counterpart of ld32
@@ -85,19 +80,62 @@ template <typename T>
 __device__ __forceinline__ float bld(buf_t r, uint32_t voff, uint32_t soff) {
   return ld(reinterpret_cast<const T*>(r.p + (voff + soff)), 0);
 }
-// four consecutive elements (16-byte aligned for f32, 8-byte for bf16)
+// A staged element: what a tile's fetch loads and the later commit converts
+// (val).  bf16 keeps its raw 16 bits in the register until then: widening
+// them next to the load would put the load's wait there, in front of the
+// tile's compute, instead of at the commit after it.
 template <typename T>
-__device__ __forceinline__ float4 bld4(buf_t r, uint32_t voff, uint32_t soff);
+struct stg;
 template <>
-__device__ __forceinline__ float4 bld4<float>(buf_t r, uint32_t voff, uint32_t soff) {
-  return *reinterpret_cast<const float4*>(r.p + (voff + soff));
+struct stg<float> {
+  float v;
+};
+template <>
+struct stg<bf16> {
+  uint16_t v;
+};
+template <typename T>
+__device__ __forceinline__ stg<T> bldr(buf_t r, uint32_t voff, uint32_t soff);
+template <>
+__device__ __forceinline__ stg<float> bldr<float>(buf_t r, uint32_t voff, uint32_t soff) {
+  return stg<float>{*reinterpret_cast<const float*>(r.p + (voff + soff))};
 }
 template <>
-__device__ __forceinline__ float4 bld4<bf16>(buf_t r, uint32_t voff, uint32_t soff) {
-  const uint2 v = *reinterpret_cast<const uint2*>(r.p + (voff + soff));
-  return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u), __uint_as_float(v.y << 16),
-                     __uint_as_float(v.y & 0xffff0000u));
+__device__ __forceinline__ stg<bf16> bldr<bf16>(buf_t r, uint32_t voff, uint32_t soff) {
+  return stg<bf16>{*reinterpret_cast<const uint16_t*>(r.p + (voff + soff))};
 }
+// element `off` of a base pointer (as ld32), staged
+template <typename T>
+__device__ __forceinline__ stg<T> ld32r(const T* base, uint32_t off) {
+  return bldr<T>(make_buf(base), off * (uint32_t)sizeof(T), 0);
+}
+__device__ __forceinline__ float val(stg<float> s) { return s.v; }
+__device__ __forceinline__ float val(stg<bf16> s) { return __uint_as_float(static_cast<uint32_t>(s.v) << 16); }
+// four consecutive elements, staged (16-byte aligned for f32, 8-byte for bf16)
+template <typename T>
+struct stg4;
+template <>
+struct stg4<float> {
+  float4 v;
+};
+template <>
+struct stg4<bf16> {
+  uint2 v;
+};
+template <typename T>
+__device__ __forceinline__ stg4<T> bld4r(buf_t r, uint32_t voff, uint32_t soff) {
+  if constexpr (sizeof(T) == 4) {
+    return stg4<T>{*reinterpret_cast<const float4*>(r.p + (voff + soff))};
+  } else {
+    return stg4<T>{*reinterpret_cast<const uint2*>(r.p + (voff + soff))};
+  }
+}
+__device__ __forceinline__ float4 val(stg4<float> s) { return s.v; }
+__device__ __forceinline__ float4 val(stg4<bf16> s) {
+  return make_float4(__uint_as_float(s.v.x << 16), __uint_as_float(s.v.x & 0xffff0000u), __uint_as_float(s.v.y << 16),
+                     __uint_as_float(s.v.y & 0xffff0000u));
+}
+
 template <typename T>
 __device__ __forceinline__ void bst(buf_t r, uint32_t voff, uint32_t soff, float v) {
   st(reinterpret_cast<T*>(const_cast<char*>(r.p) + (voff + soff)), 0, v);

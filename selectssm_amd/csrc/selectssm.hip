@@ -245,9 +245,9 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
   // LDS, so the loads' latency is covered by a whole tile.  VEC launches read
   // u and delta as 4-element vectors: thread -> rows vr, vr + 16, channels
   // vc .. vc + 3 (D % 4 == 0, so a vector is wholly inside or outside D).
-  float r_u[RPT], r_dt[RPT], r_eu[RPT], r_ez[RPT], r_B[BCE], r_C[BCE];
+  stg<T> r_u[RPT], r_dt[RPT], r_eu[RPT], r_ez[RPT], r_B[BCE], r_C[BCE];
   constexpr int VK = kTT / 16;  // vector rows per thread
-  float4 v_u[VK], v_dt[VK];
+  stg4<T> v_u[VK], v_dt[VK];
   static_assert(NT == 256 && kTT % 16 == 0, "vector staging: 16 threads per row, 16 rows per pass");
   const int vr = tid >> 4, vc = (tid & 15) * 4;
   const bool vin = cb * kBlkCh + vc < D;
@@ -258,15 +258,15 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
 #pragma unroll
       for (int k = 0; k < VK; ++k) {
         const uint32_t o = (uint32_t)min(t0 + vr + 16 * k, L - 1) * rowb + vcb;
-        v_u[k] = bld4<T>(ru, o, 0);
-        v_dt[k] = bld4<T>(rdt, o, 0);
+        v_u[k] = bld4r<T>(ru, o, 0);
+        v_dt[k] = bld4r<T>(rdt, o, 0);
       }
     } else {
 #pragma unroll
       for (int k = 0; k < RPT; ++k) {
         const int tc = min(t0 + srow0 + k * RSTEP, L - 1);  // wave-uniform
-        r_u[k] = bld<T>(ru, cb_c, (uint32_t)tc * rowb);
-        r_dt[k] = bld<T>(rdt, cb_dt, (uint32_t)(tc * dtD * sizeof(T)));
+        r_u[k] = bldr<T>(ru, cb_c, (uint32_t)tc * rowb);
+        r_dt[k] = bldr<T>(rdt, cb_dt, (uint32_t)(tc * dtD * sizeof(T)));
       }
     }
 #pragma unroll
@@ -275,8 +275,8 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
       if (BCN % NT == 0 || e < BCN) {
         const int i = e / NS, n = e - (e / NS) * NS;
         const uint32_t o = (uint32_t)(min((t0 + i) * N + min(n, N - 1), LN - 1) * sizeof(T));
-        r_B[k] = bld<T>(rB, o, 0);
-        r_C[k] = bld<T>(rC, o, 0);
+        r_B[k] = bldr<T>(rB, o, 0);
+        r_C[k] = bldr<T>(rC, o, 0);
       }
     }
     if (stage_eu || gate) {
@@ -284,8 +284,8 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
       for (int k = 0; k < RPT; ++k) {
         const int tc = min(t0 + srow0 + k * RSTEP, L - 1);
         const int pr = rev ? L - 1 - tc : tc;
-        if (stage_eu) r_eu[k] = bld<T>(ru, cb_q, (uint32_t)pr * rowb);
-        if (gate) r_ez[k] = bld<T>(rz, cb_q, (uint32_t)(pr * ldz * sizeof(T)));
+        if (stage_eu) r_eu[k] = bldr<T>(ru, cb_q, (uint32_t)pr * rowb);
+        if (gate) r_ez[k] = bldr<T>(rz, cb_q, (uint32_t)(pr * ldz * sizeof(T)));
       }
     }
   };
@@ -294,7 +294,7 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
 #pragma unroll
       for (int k = 0; k < VK; ++k) {
         const bool in = vin && t0 + vr + 16 * k < L;
-        const float4 uv = v_u[k], dr = v_dt[k];
+        const float4 uv = val(v_u[k]), dr = val(v_dt[k]);
         const float4 dv = SP ? make_float4(softplus(dr.x), softplus(dr.y), softplus(dr.z), softplus(dr.w)) : dr;
         float4* dst = reinterpret_cast<float4*>(&s_ud[buf][vr + 16 * k][vc]);
         dst[0] = in ? make_float4(uv.x, dv.x, uv.y, dv.y) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -305,15 +305,16 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
       for (int k = 0; k < RPT; ++k) {
         const int i = srow0 + k * RSTEP;
         const bool in = svalid && t0 + i < L;
-        s_ud[buf][i][scol] = in ? make_float2(r_u[k], SP ? softplus(r_dt[k]) : r_dt[k]) : make_float2(0.0f, 0.0f);
+        const float dv = SP ? softplus(val(r_dt[k])) : val(r_dt[k]);
+        s_ud[buf][i][scol] = in ? make_float2(val(r_u[k]), dv) : make_float2(0.0f, 0.0f);
       }
     }
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
       const int i = srow0 + k * RSTEP;
       const bool in = svalid && t0 + i < L;
-      if (stage_eu) s_eu[buf][i][scol] = in ? r_eu[k] : 0.0f;
-      if (gate) s_ez[buf][i][scol] = in ? r_ez[k] : 0.0f;
+      if (stage_eu) s_eu[buf][i][scol] = in ? val(r_eu[k]) : 0.0f;
+      if (gate) s_ez[buf][i][scol] = in ? val(r_ez[k]) : 0.0f;
     }
 #pragma unroll
     for (int k = 0; k < BCE; ++k) {
@@ -321,8 +322,8 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
       if (BCN % NT == 0 || e < BCN) {
         const int i = e / NS, n = e - (e / NS) * NS;
         const bool in = t0 + i < L && n < N;
-        (&s_B[buf][0][0])[e] = in ? r_B[k] : 0.0f;
-        (&s_C[buf][0][0])[e] = in ? r_C[k] : 0.0f;
+        (&s_B[buf][0][0])[e] = in ? val(r_B[k]) : 0.0f;
+        (&s_C[buf][0][0])[e] = in ? val(r_C[k]) : 0.0f;
       }
     }
   };
@@ -505,20 +506,20 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_agg_kernel(FwdArg
   const uint32_t so_c = (uint32_t)(sdc * sizeof(T)), so_dt = (uint32_t)(scol_dt * sizeof(T));
   const uint32_t rowb = (uint32_t)(D * sizeof(T)), dtrowb = (uint32_t)(dtD * sizeof(T));
 
-  float r_u[RPT], r_dt[RPT], r_B[BCE];
+  stg<T> r_u[RPT], r_dt[RPT], r_B[BCE];
   auto fetch = [&](int t0) {
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
       const int tc = min(t0 + srow0 + k * RSTEP, L - 1);  // wave-uniform
-      r_u[k] = bld<T>(ru, so_c, (uint32_t)tc * rowb);
-      r_dt[k] = bld<T>(rdt, so_dt, (uint32_t)tc * dtrowb);
+      r_u[k] = bldr<T>(ru, so_c, (uint32_t)tc * rowb);
+      r_dt[k] = bldr<T>(rdt, so_dt, (uint32_t)tc * dtrowb);
     }
 #pragma unroll
     for (int k = 0; k < BCE; ++k) {
       const int e = tid + k * NT;
       if (BCN % NT == 0 || e < BCN) {
         const int i = e / NS, n = e - (e / NS) * NS;
-        r_B[k] = bld<T>(rB, (uint32_t)(min((t0 + i) * N + min(n, N - 1), LN - 1) * sizeof(T)), 0);
+        r_B[k] = bldr<T>(rB, (uint32_t)(min((t0 + i) * N + min(n, N - 1), LN - 1) * sizeof(T)), 0);
       }
     }
   };
@@ -527,14 +528,15 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_agg_kernel(FwdArg
     for (int k = 0; k < RPT; ++k) {
       const int i = srow0 + k * RSTEP;
       const bool in = svalid && t0 + i < L;
-      s_ud[buf][i][scol] = in ? make_float2(r_u[k], SP ? softplus(r_dt[k]) : r_dt[k]) : make_float2(0.0f, 0.0f);
+      const float dv = SP ? softplus(val(r_dt[k])) : val(r_dt[k]);
+      s_ud[buf][i][scol] = in ? make_float2(val(r_u[k]), dv) : make_float2(0.0f, 0.0f);
     }
 #pragma unroll
     for (int k = 0; k < BCE; ++k) {
       const int e = tid + k * NT;
       if (BCN % NT == 0 || e < BCN) {
         const int i = e / NS, n = e - (e / NS) * NS;
-        (&s_B[buf][0][0])[e] = (t0 + i < L && n < N) ? r_B[k] : 0.0f;
+        (&s_B[buf][0][0])[e] = (t0 + i < L && n < N) ? val(r_B[k]) : 0.0f;
       }
     }
   };
@@ -743,8 +745,9 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
 
   // fetch() only issues loads; commit() (after the block's compute) masks,
   // applies softplus and the gate and writes LDS
-  float r_u[RPT], r_dt[RPT], r_dy[RPT], r_gz[RPT], r_eu[RPT], r_dyo[RPT], r_zo[RPT];
-  float r_B[BCE], r_C[BCE], r_h[SPL];
+  stg<T> r_u[RPT], r_dt[RPT], r_dy[RPT], r_gz[RPT], r_eu[RPT], r_dyo[RPT], r_zo[RPT];
+  stg<T> r_B[BCE], r_C[BCE];
+  float r_h[SPL];
   float h_next[SPL];  // checkpoint of the block staged by the last commit
   // byte offsets of this thread's staged column in a u row and an output row
   const uint32_t so_c = (uint32_t)(sdc * sizeof(T));
@@ -764,9 +767,9 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
     for (int k = 0; k < RPT; ++k) {
       const int tc = min(t0 + srow0 + k * RSTEP, L - 1);  // wave-uniform
       const int pr = rev ? L - 1 - tc : tc;              // output row of scan step tc
-      r_u[k] = bld<T>(ru, so_c, (uint32_t)tc * rowb);
-      r_dt[k] = bld<T>(rdt, so_dt, (uint32_t)(tc * dtD * sizeof(T)));
-      r_dy[k] = bld<T>(rdy, so_q, (uint32_t)pr * dyrowb);
+      r_u[k] = bldr<T>(ru, so_c, (uint32_t)tc * rowb);
+      r_dt[k] = bldr<T>(rdt, so_dt, (uint32_t)(tc * dtD * sizeof(T)));
+      r_dy[k] = bldr<T>(rdy, so_q, (uint32_t)pr * dyrowb);
     }
 #pragma unroll
     for (int k = 0; k < BCE; ++k) {
@@ -774,8 +777,8 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
       if (BCN % NT == 0 || e < BCN) {
         const int i = e / NS, n = e - (e / NS) * NS;
         const uint32_t o = (uint32_t)(min((t0 + i) * N + min(n, N - 1), LN - 1) * sizeof(T));
-        r_B[k] = bld<T>(rB, o, 0);
-        r_C[k] = bld<T>(rC, o, 0);
+        r_B[k] = bldr<T>(rB, o, 0);
+        r_C[k] = bldr<T>(rC, o, 0);
       }
     }
     if (gate || stage_eu || stage_dyo) {
@@ -783,11 +786,11 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
       for (int k = 0; k < RPT; ++k) {
         const int tc = min(t0 + srow0 + k * RSTEP, L - 1);
         const int pr = rev ? L - 1 - tc : tc;
-        if (gate) r_gz[k] = ld32(z_b, (uint32_t)(pr * ldz + sq));
-        if (stage_eu) r_eu[k] = ld32(u_b, (uint32_t)(pr * D + sq));
+        if (gate) r_gz[k] = ld32r(z_b, (uint32_t)(pr * ldz + sq));
+        if (stage_eu) r_eu[k] = ld32r(u_b, (uint32_t)(pr * D + sq));
         if (stage_dyo) {
-          r_dyo[k] = ld32(dy_b, (uint32_t)(tc * ldy + sdc));
-          if (gate) r_zo[k] = ld32(z_b, (uint32_t)(tc * ldz + sdc));
+          r_dyo[k] = ld32r(dy_b, (uint32_t)(tc * ldy + sdc));
+          if (gate) r_zo[k] = ld32r(z_b, (uint32_t)(tc * ldz + sdc));
         }
       }
     }
@@ -800,20 +803,20 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
     for (int k = 0; k < RPT; ++k) {
       const int i = srow0 + k * RSTEP;
       const bool in = svalid && t0 + i < L;
-      float dtv = r_dt[k], sg = 1.0f;
+      float dtv = val(r_dt[k]), sg = 1.0f;
       if constexpr (decltype(sp_tag)::value) {
         sg = sigmoid(dtv);
         dtv = softplus(dtv);
       }
-      const float go = in ? r_dy[k] : 0.0f;
+      const float go = in ? val(r_dy[k]) : 0.0f;
       float dyg = go;
       if (gate) {
-        const float gz = in ? r_gz[k] : 0.0f;
+        const float gz = in ? val(r_gz[k]) : 0.0f;
         s_go[buf][i][scol] = go;
         s_gz[buf][i][scol] = gz;
         dyg = go * gz * sigmoid(gz);
       }
-      s_x[buf][i][scol] = in ? make_float4(r_u[k], dtv, dyg, sg) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      s_x[buf][i][scol] = in ? make_float4(val(r_u[k]), dtv, dyg, sg) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
   };
   auto commit = [&](int buf, int blk) {
@@ -825,11 +828,11 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
     for (int k = 0; k < RPT; ++k) {
       const int i = srow0 + k * RSTEP;
       const bool in = svalid && t0 + i < L;
-      if (stage_eu) s_eu[buf][i][scol] = in ? r_eu[k] : 0.0f;
+      if (stage_eu) s_eu[buf][i][scol] = in ? val(r_eu[k]) : 0.0f;
       if (stage_dyo) {
-        float v = in ? r_dyo[k] : 0.0f;
+        float v = in ? val(r_dyo[k]) : 0.0f;
         if (gate) {
-          const float zz = r_zo[k];
+          const float zz = val(r_zo[k]);
           v *= zz * sigmoid(zz);
         }
         s_dyo[buf][i][scol] = v;
@@ -841,7 +844,7 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
       if (BCN % NT == 0 || e < BCN) {
         const int i = e / NS, n = e - (e / NS) * NS;
         const bool in = t0 + i < L && n < N;
-        const float vb = in ? r_B[k] : 0.0f, vc = in ? r_C[k] : 0.0f;
+        const float vb = in ? val(r_B[k]) : 0.0f, vc = in ? val(r_C[k]) : 0.0f;
         const int gg = n / SPL, jj = n % SPL;
 #pragma unroll
         for (int s = 0; s < SPL; ++s) {
@@ -1138,22 +1141,22 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_agg_kernel(BwdArg
   const uint32_t so_dt = (uint32_t)(scol_dt * sizeof(T)), so_q = (uint32_t)(sq * sizeof(T));
   const uint32_t dtrowb = (uint32_t)(dtD * sizeof(T)), dyrowb = (uint32_t)(ldy * sizeof(T));
   const uint32_t zrowb = (uint32_t)(ldz * sizeof(T));
-  float r_dt[RPT], r_dy[RPT], r_gz[RPT], r_C[BCE];
+  stg<T> r_dt[RPT], r_dy[RPT], r_gz[RPT], r_C[BCE];
   auto fetch = [&](int t0) {
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
       const int tc = min(t0 + srow0 + k * RSTEP, L - 1);  // wave-uniform
       const int pr = rev ? L - 1 - tc : tc;
-      r_dt[k] = bld<T>(rdt, so_dt, (uint32_t)tc * dtrowb);
-      r_dy[k] = bld<T>(rdy, so_q, (uint32_t)pr * dyrowb);
-      if (gate) r_gz[k] = bld<T>(rz, so_q, (uint32_t)pr * zrowb);
+      r_dt[k] = bldr<T>(rdt, so_dt, (uint32_t)tc * dtrowb);
+      r_dy[k] = bldr<T>(rdy, so_q, (uint32_t)pr * dyrowb);
+      if (gate) r_gz[k] = bldr<T>(rz, so_q, (uint32_t)pr * zrowb);
     }
 #pragma unroll
     for (int k = 0; k < BCE; ++k) {
       const int e = tid + k * NT;
       if (BCN % NT == 0 || e < BCN) {
         const int i = e / NS, n = e - (e / NS) * NS;
-        r_C[k] = bld<T>(rC, (uint32_t)(min((t0 + i) * N + min(n, N - 1), LN - 1) * sizeof(T)), 0);
+        r_C[k] = bldr<T>(rC, (uint32_t)(min((t0 + i) * N + min(n, N - 1), LN - 1) * sizeof(T)), 0);
       }
     }
   };
@@ -1162,10 +1165,10 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_agg_kernel(BwdArg
     for (int k = 0; k < RPT; ++k) {
       const int i = srow0 + k * RSTEP;
       const bool in = svalid && t0 + i < L;
-      const float dtv = dsp ? softplus(r_dt[k]) : r_dt[k];
-      float go = in ? r_dy[k] : 0.0f;
+      const float dtv = dsp ? softplus(val(r_dt[k])) : val(r_dt[k]);
+      float go = in ? val(r_dy[k]) : 0.0f;
       if (gate) {
-        const float gz = in ? r_gz[k] : 0.0f;
+        const float gz = in ? val(r_gz[k]) : 0.0f;
         go *= gz * sigmoid(gz);  // as the main backward pass stages it
       }
       s_dy[buf][i][scol] = in ? make_float2(dtv, go) : make_float2(0.0f, 0.0f);
@@ -1175,7 +1178,7 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_agg_kernel(BwdArg
       const int e = tid + k * NT;
       if (BCN % NT == 0 || e < BCN) {
         const int i = e / NS, n = e - (e / NS) * NS;
-        (&s_C[buf][0][0])[e] = (t0 + i < L && n < N) ? r_C[k] : 0.0f;
+        (&s_C[buf][0][0])[e] = (t0 + i < L && n < N) ? val(r_C[k]) : 0.0f;
       }
     }
   };
