@@ -168,6 +168,14 @@ __device__ __forceinline__ bool barrier_any(bool v, int* flags) {
   return any != 0;
 }
 
+// Keeps v computed at this point of the program: an empty asm statement that
+// reads and writes v in a VGPR and emits no instruction.  Arithmetic feeding
+// it cannot be moved past it, so a walk whose results are used only after a
+// long unrolled loop stays step by step, next to its LDS reads, instead of
+// being gathered after the loop (which held every step's operands in
+// registers at once).
+__device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }

@@ -569,6 +569,11 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_agg_kernel(FwdArg
         H[j] = fmaf(P[j], Bq[i % R][j] * w, H[j]);
         P[j] *= fast_exp2(A2[j] * dd);
       }
+#pragma unroll
+      for (int j = 0; j < SPL; ++j) {
+        pin(H[j]);
+        pin(P[j]);
+      }
     }
     if (more) commit(buf ^ 1, t0 - kTT);
     // products below the smallest normal float are flushed to zero; every
@@ -1208,6 +1213,11 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_agg_kernel(BwdArg
       for (int j = 0; j < SPL; ++j) {
         P[j] *= fast_exp2(A2[j] * dd);
         G[j] = fmaf(P[j], Cq[i % R][j] * dyv, G[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < SPL; ++j) {
+        pin(G[j]);
+        pin(P[j]);
       }
     }
     if (more) commit(buf ^ 1, t0 + kTT);
