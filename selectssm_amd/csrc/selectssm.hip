@@ -71,6 +71,9 @@ constexpr int kCK = SSM_CK;   // checkpoint interval = backward block length
 #ifndef SSM_FWD_PF
 #define SSM_FWD_PF 2
 #endif
+#ifndef SSM_FWD_APIPE
+#define SSM_FWD_APIPE 1  // forward: decays of step i + 1 computed during step i
+#endif
 #ifndef SSM_BWD_PF
 #define SSM_BWD_PF 1
 #endif
@@ -372,6 +375,7 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
 #pragma unroll
       for (int i = 0; i < PF; i += 2) pre(i);
       float yp[4];
+      float an[SPL];  // decays of the next step
       // epilogue operands of the current 4-step group at this lane's output
       // step, read at the group's first step so their LDS latency is covered
       float uo = 0.0f, zo = 0.0f;
@@ -406,11 +410,19 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
         }
         const float uu = ud[i % R].x, dd = ud[i % R].y;
         const float w = dd * uu;
+        float a[SPL];
+#pragma unroll
+        for (int j = 0; j < SPL; ++j) a[j] = SSM_FWD_APIPE && i > 0 ? an[j] : fast_exp2(A2[j] * dd);
+        if (SSM_FWD_APIPE && i + 1 < kTT) {
+          // the next step's decays, a step ahead of their use
+          const float dn = ud[(i + 1) % R].y;
+#pragma unroll
+          for (int j = 0; j < SPL; ++j) an[j] = fast_exp2(A2[j] * dn);
+        }
         float ys = 0.0f;
 #pragma unroll
         for (int j = 0; j < SPL; ++j) {
-          const float a = fast_exp2(A2[j] * dd);
-          h[j] = fmaf(a, h[j], Bq[i % R][j] * w);
+          h[j] = fmaf(a[j], h[j], Bq[i % R][j] * w);
           ys = j == 0 ? Cq[i % R][0] * h[0] : fmaf(Cq[i % R][j], h[j], ys);
         }
         yp[i & 3] = ys;
