@@ -893,17 +893,33 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
     auto sweeps = [&](auto full_tag) {
       constexpr bool kFull = decltype(full_tag)::value;
       float a_s[kCK][SPL], hp_s[kCK][SPL];
+      // (u, delta, dy) and B of the block kept in registers from the
+      // recompute for the adjoint where they fit (2 states per lane): the
+      // adjoint then reads only C from LDS, which is the tighter resource
+      // with 8 waves reading their operands every step
+      constexpr bool kKeepX = SPL == 2;
+      constexpr bool kKeepB = SPL == 2 && !EPI;
+      float3 x_s[kKeepX ? kCK : 1];
+      float b_s[kKeepB ? kCK : 1][SPL];
       constexpr int R = PF + 1;  // ring of operand sets, steps i .. i +- PF
       float4 xr[R];
       float bc[R][2 * SPL];
-      auto pre = [&](int i) {
-        xr[i % R] = s_x[buf][i][cw];
-        lds_vec<2 * SPL>(&s_bc[buf][i][g][sig][0], bc[i % R]);
+      auto pre = [&](int i, auto adj_tag) {
+        constexpr bool kAdj = decltype(adj_tag)::value;
+        if (!(kAdj && kKeepX)) xr[i % R] = s_x[buf][i][cw];
+        if (kAdj && kKeepB) {
+          float cv[SPL];
+          lds_vec<SPL>(&s_bc[buf][i][g][sig][SPL], cv);
+#pragma unroll
+          for (int j = 0; j < SPL; ++j) bc[i % R][SPL + j] = cv[j];
+        } else {
+          lds_vec<2 * SPL>(&s_bc[buf][i][g][sig][0], bc[i % R]);
+        }
       };
       // forward recompute of the block: a_t, h_{t-1}; dC_t = sum_d dy_t h_t;
       // with the gate, y_t for dz
 #pragma unroll
-      for (int i = 0; i < PF; ++i) pre(i);
+      for (int i = 0; i < PF; ++i) pre(i, std::false_type{});
       float yp[4];
       float vCp[SPL], vBp[SPL];  // (SSM_BWD_PIPE) the previous step's products
       // gate: operands of the current 4-step group at this lane's output
@@ -911,7 +927,7 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
       float ge_u = 0.0f, ge_z = 0.0f, ge_o = 0.0f;
 #pragma unroll
       for (int i = 0; i < kCK; ++i) {
-        if (i + PF < kCK) pre(i + PF);
+        if (i + PF < kCK) pre(i + PF, std::false_type{});
         if (gate && (i & 3) == 0) {
           const int ti = i + yrow_step(orow);
           if (skip) ge_u = stage_eu ? s_eu[buf][ti][cw] : s_x[buf][ti][cw].x;
@@ -920,6 +936,11 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
         }
         __builtin_amdgcn_sched_barrier(0);
         const float uu = xr[i % R].x, dd = xr[i % R].y, dyv = xr[i % R].z;
+        if constexpr (kKeepX) x_s[i] = make_float3(uu, dd, dyv);
+        if constexpr (kKeepB) {
+#pragma unroll
+          for (int j = 0; j < SPL; ++j) b_s[i][j] = bc[i % R][j];
+        }
         const float w = dd * uu;
         float vC[SPL];
 #pragma unroll
@@ -964,12 +985,14 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
       // adjoint, backwards through the block
       float v1p = 0.0f, v2p = 0.0f;
 #pragma unroll
-      for (int k = 0; k < PF; ++k) pre(kCK - 1 - k);
+      for (int k = 0; k < PF; ++k) pre(kCK - 1 - k, std::true_type{});
 #pragma unroll
       for (int i = kCK - 1; i >= 0; --i) {
-        if (i - PF >= 0) pre(i - PF);
+        if (i - PF >= 0) pre(i - PF, std::true_type{});
         __builtin_amdgcn_sched_barrier(0);
-        const float uu = xr[i % R].x, dd = xr[i % R].y, dyv = xr[i % R].z;
+        const float uu = kKeepX ? x_s[i].x : xr[i % R].x;
+        const float dd = kKeepX ? x_s[i].y : xr[i % R].y;
+        const float dyv = kKeepX ? x_s[i].z : xr[i % R].z;
         const float w = dd * uu;
         float s1 = 0.0f, s2 = 0.0f, vB[SPL];
 #pragma unroll
@@ -979,7 +1002,8 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
           const float qv = gg * hp_s[i][j];
           s2 = j == 0 ? Av[0] * qv : fmaf(Av[j], qv, s2);
           dAblk[j] = fmaf(dd, qv, dAblk[j]);
-          s1 = j == 0 ? bc[i % R][0] * f : fmaf(bc[i % R][j], f, s1);
+          const float Bv = kKeepB ? b_s[i][j] : bc[i % R][j];
+          s1 = j == 0 ? Bv * f : fmaf(Bv, f, s1);
           vB[j] = f * w;
           gc[j] = gg;
         }
