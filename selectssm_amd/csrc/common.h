@@ -35,15 +35,6 @@ __device__ __forceinline__ float ld<bf16>(const bf16* p, int64_t i) {
   return __uint_as_float(static_cast<uint32_t>(p[i].bits) << 16);
 }
 
-// Element `off` of a (wave-uniform) base pointer, addressed with a 32-bit byte
-// offset so the load is one SGPR-base + VGPR-offset instruction (the host
-// keeps every per-batch-row byte offset below 2^32).
-template <typename T>
-__device__ __forceinline__ float ld32(const T* base, uint32_t off) {
-  const uint32_t byte = off * (uint32_t)sizeof(T);
-  return ld(reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + byte), 0);
-}
-
 template <typename T>
 __device__ __forceinline__ void st(T* p, int64_t i, float v);
 template <>
@@ -59,7 +50,9 @@ __device__ __forceinline__ void st<bf16>(bf16* p, int64_t i, float v) {
   p[i].bits = __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
 }
 
-// store counterpart of ld32
+// Element `off` of a (wave-uniform) base pointer, addressed with a 32-bit
+// byte offset so the store is one SGPR-base + VGPR-offset instruction (the
+// host keeps every per-batch-row byte offset below 2^32).
 template <typename T>
 __device__ __forceinline__ void st32(T* base, uint32_t off, float v) {
   const uint32_t byte = off * (uint32_t)sizeof(T);
@@ -104,7 +97,7 @@ template <>
 __device__ __forceinline__ stg<bf16> bldr<bf16>(buf_t r, uint32_t voff, uint32_t soff) {
   return stg<bf16>{*reinterpret_cast<const uint16_t*>(r.p + (voff + soff))};
 }
-// element `off` of a base pointer (as ld32), staged
+// element `off` of a (wave-uniform) base pointer, staged
 template <typename T>
 __device__ __forceinline__ stg<T> ld32r(const T* base, uint32_t off) {
   return bldr<T>(make_buf(base), off * (uint32_t)sizeof(T), 0);
@@ -139,18 +132,6 @@ __device__ __forceinline__ float4 val(stg4<bf16> s) {
 template <typename T>
 __device__ __forceinline__ void bst(buf_t r, uint32_t voff, uint32_t soff, float v) {
   st(reinterpret_cast<T*>(const_cast<char*>(r.p) + (voff + soff)), 0, v);
-}
-
-// Runs f() on the lanes whose channel exists.  A workgroup whose 64 channels
-// all exist (every one when D % 64 == 0) takes a wave-uniform branch and needs
-// no per-lane exec masking.
-template <typename F>
-__device__ __forceinline__ void on_valid_lanes(bool full_block, bool valid, F&& f) {
-  if (full_block) {
-    f();
-  } else if (valid) {
-    f();
-  }
 }
 
 // Whether v holds on any lane of a workgroup of NW waves, with the barrier

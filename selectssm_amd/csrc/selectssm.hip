@@ -36,7 +36,11 @@
 // Time is walked in tiles staged in LDS: the next tile's global loads are
 // issued before the current tile computes and written to the other buffer
 // after it; inside a tile the LDS operands of step i + PF are read while step
-// i computes (sched_barrier keeps the reads where they are written).  Sums
+// i computes (sched_barrier keeps the reads where they are written).  Staged
+// bf16 values stay raw 16-bit registers until they are written to LDS (a
+// widening next to the load would wait for it there).  With 2 states per lane
+// the backward keeps the block's (u, delta, dy) and B in registers from its
+// recompute sweep, so the adjoint sweep reads only C from LDS.  Sums
 // over channel blocks (dB, dC, broadcast ddelta) and over rows / segments
 // (dA, dD) go through partial buffers reduced in a fixed order, so every
 // gradient is deterministic.
