@@ -186,6 +186,7 @@ __device__ __forceinline__ float softplus(float x) {
 // ------------------------------------------------------ cross-lane reductions
 //
 // DPP patterns used below (all within a row of 16 lanes, every lane has a source):
+//   row_newbcast:k (0x150+k) lane k of the row
 //   row_ror:8 (0x128)        lane ^ 8
 //   row_half_mirror (0x141)  lane ^ 7 within each group of 8
 //   quad_perm [2,3,0,1]      lane ^ 2
@@ -194,6 +195,31 @@ __device__ __forceinline__ float softplus(float x) {
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+
+// Lane k of each row of 16 lanes, broadcast to its row (DPP row_newbcast:k,
+// 0x150 + k, gfx90a and later).  k must be a constant after unrolling; the
+// switch then folds to one case.  A broadcast feeding a multiply becomes the
+// multiply's DPP operand (v_mul_f32_dpp), so it costs no instruction.
+__device__ __forceinline__ float row_bcast(float v, int k) {
+  switch (k & 15) {
+    case 0: return dpp_mov<0x150>(v);
+    case 1: return dpp_mov<0x151>(v);
+    case 2: return dpp_mov<0x152>(v);
+    case 3: return dpp_mov<0x153>(v);
+    case 4: return dpp_mov<0x154>(v);
+    case 5: return dpp_mov<0x155>(v);
+    case 6: return dpp_mov<0x156>(v);
+    case 7: return dpp_mov<0x157>(v);
+    case 8: return dpp_mov<0x158>(v);
+    case 9: return dpp_mov<0x159>(v);
+    case 10: return dpp_mov<0x15A>(v);
+    case 11: return dpp_mov<0x15B>(v);
+    case 12: return dpp_mov<0x15C>(v);
+    case 13: return dpp_mov<0x15D>(v);
+    case 14: return dpp_mov<0x15E>(v);
+    default: return dpp_mov<0x15F>(v);
+  }
 }
 constexpr int kDppRor8 = 0x128;
 constexpr int kDppHalfMirror = 0x141;

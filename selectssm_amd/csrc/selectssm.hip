@@ -366,15 +366,20 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
       static_assert(PF % 2 == 0, "operands are prefetched in step pairs");
       constexpr int R = PF + 2;
       float2 ud[R];
-      float Bq[R][SPL], Cq[R][SPL];
+      float Cq[R][SPL];
+      // B of the tile in registers: lane c of state row g holds B of step
+      // 16 hh + c for the row's states; step i broadcasts lane i % 16 of its
+      // row (row_bcast) straight into the B * (delta u) multiply, so B costs
+      // one LDS read per 16 steps instead of one per step
+      static_assert(kTT % 16 == 0, "B is held in 16-step register tiles");
+      float Bt[kTT / 16][SPL];
+#pragma unroll
+      for (int hh = 0; hh < kTT / 16; ++hh) lds_vec<SPL>(&s_B[buf][16 * hh + c][SPL * g], Bt[hh]);
       auto pre = [&](int i) {  // steps i, i + 1 (i even)
         ud[i % R] = s_ud[buf][i][cw];
         ud[(i + 1) % R] = s_ud[buf][i + 1][cw];
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-          lds_vec<SPL>(&s_B[buf][i + k][SPL * g], Bq[(i + k) % R]);
-          lds_vec<SPL>(&s_C[buf][i + k][SPL * g], Cq[(i + k) % R]);
-        }
+        for (int k = 0; k < 2; ++k) lds_vec<SPL>(&s_C[buf][i + k][SPL * g], Cq[(i + k) % R]);
       };
 #pragma unroll
       for (int i = 0; i < PF; i += 2) pre(i);
@@ -426,7 +431,7 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
         float ys = 0.0f;
 #pragma unroll
         for (int j = 0; j < SPL; ++j) {
-          h[j] = fmaf(a[j], h[j], Bq[i % R][j] * w);
+          h[j] = fmaf(a[j], h[j], row_bcast(Bt[i / 16][j], i) * w);
           ys = j == 0 ? Cq[i % R][0] * h[0] : fmaf(Cq[i % R][j], h[j], ys);
         }
         yp[i & 3] = ys;
