@@ -141,6 +141,23 @@ def test_bf16_io_matches_oracle():
     _compare(inp, ("skip", "gate"), dtype=torch.bfloat16, rtol=2e-2, atol=2e-2, scale_atol=True)
 
 
+@pytest.mark.parametrize("case", [
+    ((2, 77, 96, 16), ("reverse", "complement", "skip", "gate")),  # partial tile and channel block
+    ((2, 77, 98, 16), ("skip",)),                                   # D % 4 != 0: element-wise staging
+    ((1, 100, 72, 32), ("gate",)),                                  # N = 32: 8 / 4 states per lane
+    ((2, 77, 96, 16), ("softplus", "skip")),
+], ids=lambda c: "x".join(map(str, c[0])) + "-" + "+".join(c[1]))
+def test_bf16_io_variants_match_oracle(case):
+    """bf16 staging (raw 16-bit registers widened at the commit) on every staging path."""
+    shape, flags = case
+    inp = make_inputs(*shape, seed=21)
+    if "softplus" in flags:
+        inp = _pre_softplus(inp)
+    for k in ("u", "dt", "B", "C", "z", "g"):
+        inp[k] = torch.from_numpy(inp[k]).to(torch.bfloat16).float().numpy()
+    _compare(inp, flags, dtype=torch.bfloat16, rtol=2e-2, atol=2e-2, scale_atol=True)
+
+
 def test_reverse_complement_index_map_is_exact():
     """reverse(+complement) output == explicit flip of the forward scan output, bitwise."""
     from selectssm_amd import selective_scan
