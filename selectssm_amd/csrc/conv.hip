@@ -65,10 +65,46 @@ __device__ __forceinline__ float act_grad(int act, float v) {
   return 1.0f;
 }
 
+// M consecutive scan-domain steps t_lo .. t_lo + M - 1 of one column: `col`
+// points at the column's element of row 0, rows are `ld` elements apart, and
+// with `rev` step t is row L - 1 - t.  Steps outside [0, L) read as 0 (the
+// conv's causal left padding and the end of the row), and so does every step
+// when !live.  All M loads are issued at clamped, in-bounds rows before any
+// value is used, with bf16 kept as its raw 16 bits until then, so they are in
+// flight together.  (A load under a branch, or one widened next to it, gets
+// its wait on the spot: one HBM round trip per step.  The compiler sinks a
+// load whose value only a masked select uses into a branch of its own, so
+// each raw value passes an empty asm first, which makes the load
+// unconditional.)
+template <int M, typename T>
+__device__ __forceinline__ void load_rows(float (&out)[M], const T* col, int t_lo, int L, int ld, bool rev,
+                                          bool live) {
+  uint32_t raw[M];
+#pragma unroll
+  for (int j = 0; j < M; ++j) {
+    const int t = min(max(t_lo + j, 0), L - 1);
+    const int r = rev ? L - 1 - t : t;
+    const T* e = col + (int64_t)r * ld;
+    if constexpr (sizeof(T) == 4) {
+      raw[j] = *reinterpret_cast<const uint32_t*>(e);
+    } else {
+      raw[j] = *reinterpret_cast<const uint16_t*>(e);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < M; ++j) {
+    const int t = t_lo + j;
+    uint32_t v = raw[j];
+    asm volatile("" : "+v"(v));
+    const float f = sizeof(T) == 4 ? __uint_as_float(v) : __uint_as_float(v << 16);
+    out[j] = (live && t >= 0 && t < L) ? f : 0.0f;
+  }
+}
+
 template <int K, typename T>
 __global__ void __launch_bounds__(kLanes* kCW) conv_fwd_kernel(ConvArgs<T> p) {
   const int lane = threadIdx.x & (kLanes - 1);
-  const int wave = threadIdx.x / kLanes;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
   const int L = p.L, D = p.D;
   const int d = blockIdx.x * kLanes + lane;                 // scan-domain channel
   const int t0 = (blockIdx.y * kCW + wave) * kCT;           // scan-domain time
@@ -82,12 +118,7 @@ __global__ void __launch_bounds__(kLanes* kCW) conv_fwd_kernel(ConvArgs<T> p) {
   for (int k = 0; k < K; ++k) wk[k] = p.w[(int64_t)k * D + d];
   // x_s[t0 - (K-1) .. t0 + kCT - 1]
   float xs[kCT + K - 1];
-#pragma unroll
-  for (int j = 0; j < kCT + K - 1; ++j) {
-    const int t = t0 - (K - 1) + j;
-    const int r = p.rev ? L - 1 - t : t;
-    xs[j] = (t >= 0 && t < L) ? ld(xb, (int64_t)r * ldx + q) : 0.0f;
-  }
+  load_rows<kCT + K - 1>(xs, xb + q, t0 - (K - 1), L, ldx, p.rev, true);
 #pragma unroll
   for (int i = 0; i < kCT; ++i) {
     const int t = t0 + i;
@@ -103,7 +134,7 @@ __global__ void __launch_bounds__(kLanes* kCW) conv_fwd_kernel(ConvArgs<T> p) {
 template <int K, typename T>
 __global__ void __launch_bounds__(kLanes* kCW) conv_bwd_kernel(ConvArgs<T> p) {
   const int lane = threadIdx.x & (kLanes - 1);
-  const int wave = threadIdx.x / kLanes;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
   const int L = p.L, D = p.D;
   const int d = blockIdx.x * kLanes + lane;
   const int t0 = (blockIdx.y * kCW + wave) * kCT;
@@ -120,17 +151,8 @@ __global__ void __launch_bounds__(kLanes* kCW) conv_bwd_kernel(ConvArgs<T> p) {
   // x_s[t0 - (K-1) .. t0 + kCT + K - 2] and du[t0 .. t0 + kCT + K - 2]:
   // dx_s[t] needs dv at t .. t + K - 1, and dv[t] needs v[t]
   float xs[kCT + 2 * K - 2], dv[kCT + K - 1];
-#pragma unroll
-  for (int j = 0; j < kCT + 2 * K - 2; ++j) {
-    const int t = t0 - (K - 1) + j;
-    const int r = p.rev ? L - 1 - t : t;
-    xs[j] = (live && t >= 0 && t < L) ? ld(xb, (int64_t)r * ldx + q) : 0.0f;
-  }
-#pragma unroll
-  for (int j = 0; j < kCT + K - 1; ++j) {
-    const int t = t0 + j;
-    dv[j] = (live && t < L) ? ld(dub, (int64_t)t * D + dc) : 0.0f;
-  }
+  load_rows<kCT + 2 * K - 2>(xs, xb + q, t0 - (K - 1), L, ldx, p.rev, live);
+  load_rows<kCT + K - 1>(dv, dub + dc, t0, L, D, false, live);
 #pragma unroll
   for (int j = 0; j < kCT + K - 1; ++j) {
     float v = 0.0f;
