@@ -83,8 +83,27 @@ class Dense(torch.nn.Module):
     def forward(self, x):
         w = self.kernel.to(x.dtype)
         x2 = x.reshape(-1, x.shape[-1])
-        y = x2 @ w if self.bias is None else torch.addmm(self.bias.to(x.dtype), x2, w)
+        y = _DenseFn.apply(x2, w, None if self.bias is None else self.bias.to(x.dtype))
         return y.reshape(*x.shape[:-1], w.shape[1])
+
+
+class _DenseFn(torch.autograd.Function):
+    """x2 @ w + b with the weight gradient through _tn (split over the rows)."""
+
+    @staticmethod
+    def forward(ctx, x2, w, b):
+        ctx.save_for_backward(x2, w)
+        ctx.has_bias = b is not None
+        return x2 @ w if b is None else torch.addmm(b, x2, w)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, w = ctx.saved_tensors
+        dy = dy.contiguous()
+        dx = dy @ w.t() if ctx.needs_input_grad[0] else None
+        dw = _tn(x2, dy) if ctx.needs_input_grad[1] else None
+        db = dy.sum(0) if ctx.has_bias and ctx.needs_input_grad[2] else None
+        return dx, dw, db
 
 
 class _ShiftConv(torch.nn.Module):
@@ -132,6 +151,28 @@ class _FlaxModule(torch.nn.Module):
         return tree
 
 
+_TN_SLICE = 8192  # rows of K per slice of a split weight-gradient product
+
+
+def _tn(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """``a.t() @ b`` for the weight gradients, whose K = B*L is long and whose
+    M, N are a few hundred at most (e.g. (2^19 x 512)^T (2^19 x 32) for a
+    4 x 131072 BidirectionalMamba batch).  One GEMM call over that K re-reads ``a`` many times
+    (19 GB fetched for a 1 GB operand on hipBLASLt), so for float32 the K axis
+    is cut into slices of _TN_SLICE rows whose products run as one batched
+    GEMM, then summed over the slices in order: deterministic, and each
+    partial sum is shorter than the single call's.  bfloat16 keeps the single
+    call, whose output is rounded once rather than once per slice."""
+    K = a.shape[0]
+    S = K // _TN_SLICE
+    if a.dtype != torch.float32 or S < 2 or K % _TN_SLICE:
+        return a.t() @ b
+    a3 = a.reshape(S, _TN_SLICE, a.shape[1])
+    b3 = b.reshape(S, _TN_SLICE, b.shape[1])
+    # (S, N, M): the transposed view is the left operand, the right one is contiguous
+    return torch.bmm(b3.transpose(1, 2), a3).sum(0).t()
+
+
 def _core_forward(u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, Dp, z, N, rank, reverse, complement, y_out=None):
     """Projections + scan (selectssm.py:190-238); returns (y, saved tensors)."""
     B_, L_, D = u.shape
@@ -160,18 +201,18 @@ def _core_backward(saved, dy, N, rank, reverse, complement):
     u2 = u.reshape(-1, D)
     du2 = du.reshape(-1, D)
     dBC = torch.cat([dB.reshape(-1, N), dC.reshape(-1, N)], dim=1)
-    dWbc = u2.t() @ dBC
+    dWbc = _tn(u2, dBC)
     dbbc = dBC.sum(0)
     du2.addmm_(dBC, Wbc.to(u.dtype).t())  # u's gradient through BC, accumulated in place
     if Wp is not None:
         ddt2 = ddt.reshape(-1, D)
-        dWp = (dt_low.t() @ ddt2).to(Wp.dtype)
+        dWp = _tn(dt_low, ddt2).to(Wp.dtype)
         dbp = ddt2.sum(0).to(Wp.dtype)
         ddt_low = ddt2 @ Wp.to(u.dtype).t()
     else:
         dWp = dbp = None
         ddt_low = ddt.reshape(-1, rank, D // rank).sum(-1) if rank > 1 else ddt.reshape(-1, 1)
-    dWdt = u2.t() @ ddt_low
+    dWdt = _tn(u2, ddt_low)
     dbdt = ddt_low.sum(0)
     du2.addmm_(ddt_low, Wdt.to(u.dtype).t())  # and through dt
     dA_log = dA * A  # A = -exp(A_log)

@@ -87,3 +87,20 @@ def test_synthetic_inputs_follow_the_config_distributions():
     assert abs(float(x["B"].std()) - 0.25) < 0.01
     y = make_inputs(2, 512, 64, 16, seed=0)
     assert all(np.array_equal(x[k], y[k]) for k in x)
+
+
+@pytest.mark.parametrize("K,M,N,dtype", [(3 * 8192, 40, 24, torch.float32), (8192 + 8, 16, 8, torch.float32),
+                                         (2 * 8192, 16, 8, torch.bfloat16), (100, 7, 5, torch.float32)])
+def test_split_weight_gradient_product(K, M, N, dtype):
+    """The modules' weight-gradient product a^T b: split over K into slices (float32,
+    K a multiple of the slice) or one call (otherwise) -- the same matrix."""
+    from selectssm_amd.modules import _tn
+
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn(K, M, generator=g).to(dtype)
+    b = torch.randn(K, N, generator=g).to(dtype)
+    ref = a.double().t() @ b.double()
+    got = _tn(a, b)
+    assert got.shape == (M, N) and got.dtype == dtype
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    assert torch.allclose(got.double(), ref, rtol=tol, atol=tol * float(ref.abs().max()))
