@@ -750,10 +750,16 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
   __shared__ float4 s_x[2][kCK][kBlkCh];  // (u, delta, dy of the scan, softplus'(delta) or 1)
   // (B, C) of each step in the state order of each lane class: [t][group][sig][B slots, C slots]
   __shared__ __attribute__((aligned(16))) float s_bc[2][kCK][8][SPL][2 * SPL];
-  __shared__ float s_dB[kBwdWaves][kCK][NS], s_dC[kBwdWaves][kCK][NS];  // per-wave channel sums
+  // per-wave channel sums, in two sets where LDS allows (all but N > 16 with
+  // the gate): a block's totals are then added after the one barrier that
+  // also publishes the next block's staged operands, while the next block's
+  // sweeps write the other set
+  constexpr int kSB = (SPL == 4 && EPI) ? 1 : 2;
+  int sb = 0;
+  __shared__ float s_dB[kSB][kBwdWaves][kCK][NS], s_dC[kSB][kBwdWaves][kCK][NS];
   __shared__ float s_go[EB][ER][kBlkCh], s_gz[EB][ER][kBlkCh];  // gate: raw dy and z at the output position
   __shared__ float s_eu[EB][ER][kBlkCh], s_dyo[EB][ER][kBlkCh];
-  __shared__ float s_ddt[kBwdWaves][kCK];  // broadcast delta: per-wave channel sums of ddelta
+  __shared__ float s_ddt[kSB][kBwdWaves][kCK];  // broadcast delta: per-wave channel sums of ddelta
 
   const int dtD = p.dstride ? D : 1;
   const int scol_dt = p.dstride ? sdc : 0;
@@ -961,12 +967,12 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
           vC[j] = dyv * h[j];
         }
         if constexpr (SSM_BWD_PIPE) {
-          if (i > 0) s_dC[wave][i - 1][SPL * g + sig] = chan_reduce8<SPL>(vCp);
+          if (i > 0) s_dC[sb][wave][i - 1][SPL * g + sig] = chan_reduce8<SPL>(vCp);
 #pragma unroll
           for (int j = 0; j < SPL; ++j) vCp[j] = vC[j];
-          if (i == kCK - 1) s_dC[wave][i][SPL * g + sig] = chan_reduce8<SPL>(vCp);
+          if (i == kCK - 1) s_dC[sb][wave][i][SPL * g + sig] = chan_reduce8<SPL>(vCp);
         } else {
-          s_dC[wave][i][SPL * g + sig] = chan_reduce8<SPL>(vC);
+          s_dC[sb][wave][i][SPL * g + sig] = chan_reduce8<SPL>(vC);
         }
         if (gate) {
           float ys = bc[i % R][SPL] * h[0];
@@ -1017,12 +1023,12 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
           gc[j] = gg;
         }
         if constexpr (SSM_BWD_PIPE) {
-          if (i < kCK - 1) s_dB[wave][i + 1][SPL * g + sig] = chan_reduce8<SPL>(vBp);
+          if (i < kCK - 1) s_dB[sb][wave][i + 1][SPL * g + sig] = chan_reduce8<SPL>(vBp);
 #pragma unroll
           for (int j = 0; j < SPL; ++j) vBp[j] = vB[j];
-          if (i == 0) s_dB[wave][0][SPL * g + sig] = chan_reduce8<SPL>(vBp);
+          if (i == 0) s_dB[sb][wave][0][SPL * g + sig] = chan_reduce8<SPL>(vBp);
         } else {
-          s_dB[wave][i][SPL * g + sig] = chan_reduce8<SPL>(vB);
+          s_dB[sb][wave][i][SPL * g + sig] = chan_reduce8<SPL>(vB);
         }
         // du = delta sum_n f B; ddelta = sum_n f (A a h_{t-1} + B u)
         const float v1 = dd * s1, v2 = fmaf(uu, s1, s2);
@@ -1060,7 +1066,7 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
             float sv = val + dpp_mov<kDppHalfMirror>(val);
             sv += dpp_mov<kDppXor2>(sv);
             sv += dpp_mov<kDppXor1>(sv);
-            if (!is_du && lead && c == 0) s_ddt[wave][ti] = sv;
+            if (!is_du && lead && c == 0) s_ddt[sb][wave][ti] = sv;
           }
         }
       }
@@ -1078,8 +1084,8 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
       dDacc += dDmid;
       dDmid = 0.0f;
     }
-    __syncthreads();
     // dB, dC totals of this channel block: the 8 waves' sums added in order
+    auto totals = [&]() {
     for (int e = tid; e < 2 * kCK * NS; e += NT) {
       const int which = e / (kCK * NS);
       const int r = e - which * (kCK * NS);
@@ -1087,7 +1093,7 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
       if (n < N && t0 + i < L) {
         float s = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kBwdWaves; ++w) s += which ? s_dC[w][i][n] : s_dB[w][i][n];
+        for (int w = 0; w < kBwdWaves; ++w) s += which ? s_dC[sb][w][i][n] : s_dB[sb][w][i][n];
         float* dst = which ? p.ws_dC : p.ws_dB;
         dst[(((int64_t)cb * p.Bt + b) * L + t0 + i) * N + n] = s;
       }
@@ -1095,11 +1101,21 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
     if (BC && tid < kCK && t0 + tid < L) {
       float s = 0.0f;
 #pragma unroll
-      for (int w = 0; w < kBwdWaves; ++w) s += s_ddt[w][tid];
+      for (int w = 0; w < kBwdWaves; ++w) s += s_ddt[sb][w][tid];
       p.ws_ddt[((int64_t)cb * p.Bt + b) * L + t0 + tid] = s;
     }
-    if (more) commit(buf ^ 1, blk - 1);
-    __syncthreads();
+    };
+    if constexpr (kSB == 2) {
+      if (more) commit(buf ^ 1, blk - 1);
+      __syncthreads();
+      totals();
+      sb ^= 1;
+    } else {
+      __syncthreads();
+      totals();
+      if (more) commit(buf ^ 1, blk - 1);
+      __syncthreads();
+    }
   }
 
 #pragma unroll
