@@ -157,8 +157,8 @@ _TN_SLICE = 8192  # rows of K per slice of a split weight-gradient product
 def _tn(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     """``a.t() @ b`` for the weight gradients, whose K = B*L is long and whose
     M, N are a few hundred at most (e.g. (2^19 x 512)^T (2^19 x 32) for a
-    4 x 131072 BidirectionalMamba batch).  One GEMM call over that K re-reads ``a`` many times
-    (19 GB fetched for a 1 GB operand on hipBLASLt), so for float32 the K axis
+    4 x 131072 BidirectionalMamba batch).  One GEMM call over that K re-reads
+    ``a`` many times (19 GB fetched for a 1 GB operand on hipBLASLt), so for float32 the K axis
     is cut into slices of _TN_SLICE rows whose products run as one batched
     GEMM, then summed over the slices in order: deterministic, and each
     partial sum is shorter than the single call's.  bfloat16 keeps the single
@@ -218,6 +218,31 @@ def _core_backward(saved, dy, N, rank, reverse, complement):
     dA_log = dA * A  # A = -exp(A_log)
     f32 = lambda g: g.to(torch.float32)
     return du, dA_log, f32(dWbc), f32(dbbc), f32(dWdt), f32(dbdt), dWp, dbp, dD, dz
+
+
+class _SplitCols(torch.autograd.Function):
+    """Consecutive column blocks of ``h`` (``jnp.split`` of in_proj's output,
+    selectssm.py:319), returned as views.  Slicing ``h`` directly gives each
+    block a zero-filled gradient of h's full shape, which autograd then adds
+    up; this backward writes the blocks' gradients side by side into one."""
+
+    @staticmethod
+    def forward(ctx, h, *widths):
+        if sum(widths) != h.shape[-1]:
+            raise ValueError(f"column blocks {widths} do not cover the last dimension {h.shape[-1]}")
+        ctx.widths = widths
+        outs, o = [], 0
+        for w in widths:
+            outs.append(h[..., o:o + w])
+            o += w
+        return tuple(outs)
+
+    @staticmethod
+    def backward(ctx, *grads):
+        ref = next(g for g in grads if g is not None)
+        parts = [g if g is not None else torch.zeros(*ref.shape[:-1], w, dtype=ref.dtype, device=ref.device)
+                 for g, w in zip(grads, ctx.widths)]
+        return (torch.cat(parts, dim=-1), *([None] * len(ctx.widths)))
 
 
 class _SSMCoreFn(torch.autograd.Function):
@@ -605,10 +630,11 @@ class BidirectionalMamba(_FlaxModule):
         n_in = 1 if self.tie_in_proj else 2
         h = self.in_proj(x)
         # jnp.split at [ED, n_in*ED, (n_in+1)*ED] (selectssm.py:319-321)
-        xf, _xr = h[..., :ED], h[..., ED:n_in * ED]
-        zf, _zr = h[..., n_in * ED:(n_in + 1) * ED], h[..., (n_in + 1) * ED:]
-        xr = xf if self.tie_in_proj else _xr
-        zr = zf if self.tie_gate else _zr
+        n_gate = 1 if self.tie_gate else 2
+        blocks = _SplitCols.apply(h, *([ED] * (n_in + n_gate)))
+        xf, zf = blocks[0], blocks[n_in]
+        xr = xf if self.tie_in_proj else blocks[1]
+        zr = zf if self.tie_gate else blocks[n_in + 1]
         # the gate of selectssm.py:335-336 is applied inside each SSM's scan
         # epilogue; xf, xr, zf, zr are read in place from in_proj's output
         if (self.concatenate_fwd_rev and self.activation == "silu" and not self.ssm_fwd._unfused_outputs()

@@ -104,3 +104,22 @@ def test_split_weight_gradient_product(K, M, N, dtype):
     assert got.shape == (M, N) and got.dtype == dtype
     tol = 1e-4 if dtype == torch.float32 else 2e-2
     assert torch.allclose(got.double(), ref, rtol=tol, atol=tol * float(ref.abs().max()))
+
+
+def test_split_columns_views_and_gradient():
+    """in_proj's output split into column blocks: the blocks are views of h, and
+    the gradient of h is the blocks' gradients side by side (zeros for an unused block)."""
+    from selectssm_amd.modules import _SplitCols
+
+    h = torch.randn(2, 5, 12, dtype=torch.float64, requires_grad=True)
+    a, b, c = _SplitCols.apply(h, 4, 4, 4)
+    assert a.data_ptr() == h.data_ptr() and c.data_ptr() == h.data_ptr() + 8 * 8
+    (2 * a.sum() + (c * c).sum()).backward()
+    ref = torch.zeros_like(h)
+    ref[..., :4] = 2
+    ref[..., 8:] = 2 * h.detach()[..., 8:]
+    assert torch.equal(h.grad, ref)
+    assert torch.autograd.gradcheck(lambda t: _SplitCols.apply(t, 3, 9),
+                                    (torch.randn(2, 3, 12, dtype=torch.float64, requires_grad=True),))
+    with pytest.raises(ValueError):
+        _SplitCols.apply(h, 4, 4)
