@@ -490,8 +490,8 @@ class RMSNorm(torch.nn.Module):
         self.scale = torch.nn.Parameter(torch.ones(D, device=device))
 
     def forward(self, x):
-        xf = x.float()
-        y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps) * self.scale
+        # x * rsqrt(mean(x^2) + eps) * scale over the last axis, as one op
+        y = F.rms_norm(x.float(), (x.shape[-1],), self.scale, self.eps)
         return y.to(x.dtype)
 
 
