@@ -72,18 +72,27 @@ def test_conv_flip_maps_are_exact():
     assert torch.equal(conv1d_act(xt, wt, complement=True), conv1d_act(xt, wt))
 
 
-def test_conv_bf16_matches_oracle():
-    x, w, g = _inputs(2, 256, 128, 4, seed=5)
+@pytest.mark.parametrize("shape,rev,comp", [((2, 256, 128, 4), False, False), ((1, 1, 3, 4), False, False),
+                                            ((1, 3, 5, 4), True, True), ((2, 300, 70, 4), True, False),
+                                            ((1, 129, 64, 3), True, True), ((2, 1000, 130, 8), False, False)],
+                         ids=lambda v: "x".join(map(str, v)) if isinstance(v, tuple) else str(v))
+def test_conv_bf16_matches_oracle(shape, rev, comp):
+    """bf16 I/O: rows shorter than the kernel, partial time tiles and channel
+    blocks, both flip maps (every load of a thread's window is issued at a
+    clamped row and masked afterwards)."""
+    B, L, D, K = shape
+    print(f"conv bf16 shape={shape} rev={rev} comp={comp}", flush=True)
+    x, w, g = _inputs(B, L, D, K, seed=5 + sum(shape))
     xb = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
     gb = torch.from_numpy(g).to(torch.bfloat16).float().numpy()
-    u, dx, dw = _run(xb, w, gb, dtype=torch.bfloat16)
-    w2 = w.reshape(4, 128)
-    ru = O.conv_act_forward(xb, w2)
-    rdx, rdw = O.conv_act_backward(xb, w2, gb)
+    u, dx, dw = _run(xb, w, gb, dtype=torch.bfloat16, reverse=rev, complement=comp)
+    w2 = w.reshape(K, D)
+    ru = O.conv_act_forward(xb, w2, "silu", rev, comp)
+    rdx, rdw = O.conv_act_backward(xb, w2, gb, "silu", rev, comp)
     at = lambda r: 2e-2 * max(1.0, float(np.abs(r).max()))
     _close("u", u, ru, 2e-2, at(ru))
     _close("dx", dx, rdx, 2e-2, at(rdx))
-    _close("dw", dw.reshape(4, 128), rdw, 2e-2, at(rdw))
+    _close("dw", dw.reshape(K, D), rdw, 2e-2, at(rdw))
 
 
 def test_conv_deterministic_and_partial_grads():
