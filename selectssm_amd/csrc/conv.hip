@@ -197,20 +197,25 @@ __global__ void __launch_bounds__(kLanes* kCW) conv_bwd_kernel(ConvArgs<T> p) {
   }
 }
 
-// out[i] = sum over parts k of ws[k*count + i]: a workgroup takes 64
-// consecutive columns; its 16 lane groups sum the parts k = g, g + 16, ... in
-// order, and the 16 group sums are added in order through LDS (a fixed order
-// overall, so dw is deterministic)
-constexpr int kRedCols = 64, kRedGroups = 16;
+// out[y*count + i] = sum over parts k in [y*per, min(nparts, (y+1)*per)) of
+// ws[k*count + i], y = blockIdx.y: a workgroup takes 64 consecutive columns;
+// its 16 lane groups sum the parts k0 + g, k0 + g + 16, ... in order, and the
+// 16 group sums are added in order through LDS (a fixed order overall, so dw
+// is deterministic).  Many parts (long rows) go through two launches: slices
+// of kRedSlice parts into a staging area, then the slices.
+constexpr int kRedCols = 64, kRedGroups = 16, kRedSlice = 64;
 __global__ void __launch_bounds__(kRedCols* kRedGroups) conv_reduce_kernel(const float* __restrict__ ws,
                                                                           float* __restrict__ out, int nparts,
-                                                                          int64_t count) {
+                                                                          int per, int64_t count) {
   const int col = threadIdx.x % kRedCols;
   const int grp = threadIdx.x / kRedCols;
   const int64_t i = (int64_t)blockIdx.x * kRedCols + col;
+  const int k0 = blockIdx.y * per;
+  const int k1 = min(nparts, k0 + per);
+  out += (int64_t)blockIdx.y * count;
   float s = 0.0f;
   if (i < count)
-    for (int k = grp; k < nparts; k += kRedGroups) s += ws[(int64_t)k * count + i];
+    for (int k = k0 + grp; k < k1; k += kRedGroups) s += ws[(int64_t)k * count + i];
   __shared__ float part[kRedGroups][kRedCols];
   part[grp][col] = s;
   __syncthreads();
@@ -225,6 +230,13 @@ __global__ void __launch_bounds__(kRedCols* kRedGroups) conv_reduce_kernel(const
 struct ConvShape {
   int B, L, D, K, ntile, ldx;
 };
+
+// slices of the first reduction launch (0: one launch over all parts; also
+// when the slices would not fit a grid's y dimension)
+int red_slices(int64_t nparts) {
+  const int64_t S = (nparts + kRedSlice - 1) / kRedSlice;
+  return nparts > kRedSlice && S <= 65535 ? (int)S : 0;
+}
 
 int validate_conv(const ssm_conv_desc_t* desc, ConvShape* s) {
   if (desc == nullptr) return fail(SSM_ERR_INVALID, "desc is NULL");
@@ -312,9 +324,22 @@ int launch_conv_bwd(hipStream_t st, const ssm_conv_desc_t* desc, const ConvShape
   if (int rc = hip_check(hipGetLastError(), "ssm_conv_bwd launch")) return rc;
   if (dw != nullptr) {
     const int64_t count = (int64_t)s.K * s.D;
-    hipLaunchKernelGGL(conv_reduce_kernel, dim3((unsigned)((count + kRedCols - 1) / kRedCols)),
-                       dim3(kRedCols * kRedGroups), 0, st, static_cast<const float*>(workspace), dw, s.B * s.ntile,
-                       count);
+    const int nparts = s.B * s.ntile;
+    const int S = red_slices(nparts);
+    const unsigned gx = (unsigned)((count + kRedCols - 1) / kRedCols);
+    const float* parts = static_cast<const float*>(workspace);
+    if (S > 0) {
+      // slices of kRedSlice parts into the staging area after the parts
+      float* stage = static_cast<float*>(workspace) + (int64_t)nparts * count;
+      hipLaunchKernelGGL(conv_reduce_kernel, dim3(gx, (unsigned)S), dim3(kRedCols * kRedGroups), 0, st, parts, stage,
+                         nparts, kRedSlice, count);
+      if (int rc = hip_check(hipGetLastError(), "ssm_conv_bwd reduce launch")) return rc;
+      hipLaunchKernelGGL(conv_reduce_kernel, dim3(gx, 1u), dim3(kRedCols * kRedGroups), 0, st,
+                         static_cast<const float*>(stage), dw, S, S, count);
+    } else {
+      hipLaunchKernelGGL(conv_reduce_kernel, dim3(gx, 1u), dim3(kRedCols * kRedGroups), 0, st, parts, dw, nparts,
+                         nparts, count);
+    }
     return hip_check(hipGetLastError(), "ssm_conv_bwd reduce launch");
   }
   return SSM_OK;
@@ -328,7 +353,8 @@ size_t ssm_conv_bwd_workspace_bytes(const ssm_conv_desc_t* desc) {
   g_last_error.clear();
   ConvShape s;
   if (validate_conv(desc, &s)) return 0;
-  return (size_t)s.B * s.ntile * s.K * s.D * sizeof(float);
+  const int64_t nparts = (int64_t)s.B * s.ntile;
+  return (size_t)(nparts + red_slices(nparts)) * s.K * s.D * sizeof(float);
 }
 
 int ssm_conv_fwd(void* stream, const ssm_conv_desc_t* desc, const void* x, const float* w, void* u) {

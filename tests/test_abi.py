@@ -123,6 +123,9 @@ def test_conv_desc_validation():
     d = L.SsmConvDesc(**good)
     # dw partial sums: one (K, D) slab per (batch row, 128-step tile)
     assert lib.ssm_conv_bwd_workspace_bytes(ctypes.byref(d)) == 2 * 1 * 4 * 64 * 4
+    # more than 64 slabs: plus a staging area of one slab per 64 for the two-launch reduction
+    long = L.SsmConvDesc(**dict(good, seqlen=128 * 100))
+    assert lib.ssm_conv_bwd_workspace_bytes(ctypes.byref(long)) == (200 + 4) * 4 * 64 * 4
     for field, value, msg in [("ksize", 0, b"ksize"), ("ksize", 9, b"ksize"), ("activation", 3, b"activation"),
                               ("flags", L.SSM_SKIP, b"conv flags"), ("flags", L.SSM_COMPLEMENT, b"COMPLEMENT"),
                               ("dtype", 5, b"dtype"), ("seqlen", 0, b"seqlen"), ("ld_x", 8, b"ld_x")]:
