@@ -135,6 +135,7 @@ def module_bench(args):
     def step():
         for p in params:
             p.grad = None
+        x.grad = None  # the input's gradient is produced every step, not accumulated over steps
         h = embed(x) if embed is not None else x.requires_grad_(True)
         y = model(h)
         grad = torch.ones_like(y) if args.config != 2 else torch.randn_like(y, generator=g)
