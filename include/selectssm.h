@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define SSM_ABI_VERSION 3
+#define SSM_ABI_VERSION 4
 
 /* error codes */
 #define SSM_OK 0
@@ -123,6 +123,32 @@ int ssm_bwd(void* stream, const ssm_desc_t* desc,
             const float* ckpt, const void* dy,
             void* du, void* ddelta, float* dA, void* dB, void* dC,
             float* dD, void* dz, void* workspace);
+
+/* Buffers of one ssm_fwd call (same meaning and requirements). */
+typedef struct {
+  const void* u; const void* delta; const float* A; const void* B; const void* C;
+  const float* D; const void* z; void* y; float* ckpt; void* workspace;
+} ssm_fwd_io_t;
+
+/* Buffers of one ssm_bwd call (same meaning and requirements). */
+typedef struct {
+  const void* u; const void* delta; const float* A; const void* B; const void* C;
+  const float* D; const void* z; const float* ckpt; const void* dy;
+  void* du; void* ddelta; float* dA; void* dB; void* dC; float* dD; void* dz; void* workspace;
+} ssm_bwd_io_t;
+
+/*
+ * Two scans, desc[k] with io[k] for k = 0, 1: the same results as ssm_fwd
+ * (resp. ssm_bwd) called for each in turn.  Replaces the forward and reverse
+ * SSM calls of BidirectionalMamba (selectssm.py:325-326): when both descs
+ * have the same shape (batch, seqlen, dim, dstate, dtype, delta_broadcast,
+ * segments and SSM_DELTA_SOFTPLUS) and their rows are split in time, the
+ * time-split aggregate passes of both run in one launch.  Each call keeps its
+ * own time segments, so the results are bitwise those of the two calls.  The
+ * two calls must not share an output or workspace buffer.
+ */
+int ssm_fwd_pair(void* stream, const ssm_desc_t* desc, const ssm_fwd_io_t* io);
+int ssm_bwd_pair(void* stream, const ssm_desc_t* desc, const ssm_bwd_io_t* io);
 
 /* ------------------------------------------------------------------------
  * Causal depthwise conv1d + activation: the step before the scan

@@ -28,7 +28,7 @@ SSM_ACT_NONE = 0
 SSM_ACT_SILU = 1
 SSM_ACT_RELU = 2
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # every symbol include/selectssm.h declares
 EXPORTS = (
@@ -39,6 +39,8 @@ EXPORTS = (
     "ssm_bwd_workspace_bytes",
     "ssm_fwd",
     "ssm_bwd",
+    "ssm_fwd_pair",
+    "ssm_bwd_pair",
     "ssm_conv_bwd_workspace_bytes",
     "ssm_conv_fwd",
     "ssm_conv_bwd",
@@ -60,6 +62,22 @@ class SsmDesc(ctypes.Structure):
         ("ld_y", ctypes.c_int64),
         ("ld_z", ctypes.c_int64),
     ]
+
+
+_vp = ctypes.c_void_p
+
+
+class SsmFwdIo(ctypes.Structure):
+    """Mirror of ``ssm_fwd_io_t``."""
+
+    _fields_ = [(n, _vp) for n in ("u", "delta", "A", "B", "C", "D", "z", "y", "ckpt", "workspace")]
+
+
+class SsmBwdIo(ctypes.Structure):
+    """Mirror of ``ssm_bwd_io_t``."""
+
+    _fields_ = [(n, _vp) for n in ("u", "delta", "A", "B", "C", "D", "z", "ckpt", "dy", "du", "ddelta", "dA", "dB",
+                                   "dC", "dD", "dz", "workspace")]
 
 
 class SsmConvDesc(ctypes.Structure):
@@ -106,6 +124,10 @@ def _declare(lib):
     lib.ssm_fwd.argtypes = [vp, dp, vp, vp, fp, vp, vp, fp, vp, vp, fp, vp]
     lib.ssm_bwd.restype = ctypes.c_int
     lib.ssm_bwd.argtypes = [vp, dp, vp, vp, fp, vp, vp, fp, vp, fp, vp, vp, vp, fp, vp, vp, fp, vp, vp]
+    lib.ssm_fwd_pair.restype = ctypes.c_int
+    lib.ssm_fwd_pair.argtypes = [vp, dp, ctypes.POINTER(SsmFwdIo)]
+    lib.ssm_bwd_pair.restype = ctypes.c_int
+    lib.ssm_bwd_pair.argtypes = [vp, dp, ctypes.POINTER(SsmBwdIo)]
     cp = ctypes.POINTER(SsmConvDesc)
     lib.ssm_conv_bwd_workspace_bytes.restype = ctypes.c_size_t
     lib.ssm_conv_bwd_workspace_bytes.argtypes = [cp]

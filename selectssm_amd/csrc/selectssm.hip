@@ -476,7 +476,7 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
 // exact zeros and the walk stops there: with decaying states only the last
 // few thousand steps of a long segment are read.
 template <int SPL, bool SP, typename T>
-__global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_agg_kernel(FwdArgs<T> p) {
+__device__ __forceinline__ void fwd_agg_body(const FwdArgs<T>& p, const int b) {
   constexpr int NS = 4 * SPL;
   constexpr int NT = FwdStage::NT, RPT = FwdStage::RPT, RSTEP = FwdStage::RSTEP;
   constexpr int BCN = kTT * NS;
@@ -487,7 +487,7 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_agg_kernel(FwdArg
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 15;
   const int g = lane >> 4;
-  const int b = blockIdx.y;
+  // b: the batch row (blockIdx.y of a single launch)
   const int cb = blockIdx.x;
   const int seg = blockIdx.z;
   const int L = p.L, D = p.D, N = p.N;
@@ -613,6 +613,17 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_agg_kernel(FwdArg
       p.agg_P[(o * N + SPL * g + j) * D + d] = P[j];
     }
   }
+}
+
+// Workgroups with blockIdx.y < rows0 aggregate rows of p0, the others rows of
+// p1 (blockIdx.y - rows0): both directions of a BidirectionalMamba pass run
+// their aggregate walks in one launch.  A single launch passes p0 twice.
+template <int SPL, bool SP, typename T>
+__global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_agg_kernel(FwdArgs<T> p0, FwdArgs<T> p1,
+                                                                         int rows0) {
+  const int y = blockIdx.y;
+  if (y < rows0) fwd_agg_body<SPL, SP, T>(p0, y);
+  else fwd_agg_body<SPL, SP, T>(p1, y - rows0);
 }
 
 // -------------------------------------------------------------- backward
@@ -1146,7 +1157,7 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
 // so once every P of the workgroup is 0 (flushed at tile ends, flush_tiny) all
 // later steps add exact zeros and the walk stops there.
 template <int SPL, bool EPI, typename T>
-__global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_agg_kernel(BwdArgs<T> p) {
+__device__ __forceinline__ void bwd_agg_body(const BwdArgs<T>& p, const int b) {
   constexpr int NS = 8 * SPL;
   constexpr int NT = kWave * kBwdWaves;
   constexpr int RPT = kTT * kBlkCh / NT;
@@ -1159,7 +1170,7 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_agg_kernel(BwdArg
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 7;
   const int g = lane >> 3;
-  const int b = blockIdx.y;
+  // b: the batch row (blockIdx.y of a single launch)
   const int cb = blockIdx.x;
   const int seg = blockIdx.z + 1;
   const int L = p.L, D = p.D, N = p.N;
@@ -1297,6 +1308,15 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_agg_kernel(BwdArg
       p.agg_P[(o * N + SPL * g + j) * D + d] = P[j];
     }
   }
+}
+
+// As ssm_fwd_agg_kernel: rows of p0 below rows0, rows of p1 above.
+template <int SPL, bool EPI, typename T>
+__global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_agg_kernel(BwdArgs<T> p0, BwdArgs<T> p1,
+                                                                         int rows0) {
+  const int y = blockIdx.y;
+  if (y < rows0) bwd_agg_body<SPL, EPI, T>(p0, y);
+  else bwd_agg_body<SPL, EPI, T>(p1, y - rows0);
 }
 
 // out[i] = sum_k ws[k*count + i], k = 0..nparts-1 in order.  Each thread sums
@@ -1450,9 +1470,9 @@ WsLayout ws_layout(const Shape& s, bool bcast) {
 }
 
 template <typename T>
-int launch_fwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const void* u, const void* delta,
-               const float* A, const void* Bc, const void* Cc, const float* Dskip, const void* z, void* y,
-               float* ckpt, void* workspace) {
+FwdArgs<T> fwd_args(const ssm_desc_t* desc, const Shape& s, const void* u, const void* delta, const float* A,
+                    const void* Bc, const void* Cc, const float* Dskip, const void* z, void* y, float* ckpt,
+                    void* workspace) {
   FwdArgs<T> a;
   a.u = static_cast<const T*>(u);
   a.delta = static_cast<const T*>(delta);
@@ -1474,17 +1494,38 @@ int launch_fwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const voi
   a.ldy = s.ldy;
   a.ldz = s.ldz;
   a.dstride = desc->delta_broadcast ? 0 : 1;
-  const bool vec = s.D % 4 == 0 && !desc->delta_broadcast && reinterpret_cast<uintptr_t>(u) % (4 * sizeof(T)) == 0 &&
-                   reinterpret_cast<uintptr_t>(delta) % (4 * sizeof(T)) == 0;
   a.flags = desc->flags;
+  return a;
+}
+
+// Aggregates of every segment but the last (s.nseg > 1): rows of a0, and with
+// a pair (rows = 2 * s.B) the rows of a1 in the same launch.
+template <typename T>
+int launch_fwd_agg(hipStream_t st, const Shape& s, const FwdArgs<T>& a0, const FwdArgs<T>& a1, int rows) {
+  if (!dispatch_spl<4, 8>(s.spl_f, false, [&](auto spl, auto) {
+        constexpr int S = decltype(spl)::value;
+        auto go = [&](auto sp) {
+          constexpr bool SP = decltype(sp)::value;
+          hipLaunchKernelGGL((ssm_fwd_agg_kernel<S, SP, T>), dim3(s.ncb, rows, s.nseg - 1), dim3(kWave * kFwdWaves),
+                             0, st, a0, a1, s.B);
+        };
+        if (a0.flags & SSM_DELTA_SOFTPLUS) go(std::true_type{}); else go(std::false_type{});
+      }))
+    return fail(SSM_ERR_UNSUPPORTED, "no kernel variant for this shape");
+  return hip_check(hipGetLastError(), "ssm_fwd aggregate launch");
+}
+
+template <typename T>
+int launch_fwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const FwdArgs<T>& a, bool with_agg) {
+  if (with_agg && s.nseg > 1)
+    if (int rc = launch_fwd_agg<T>(st, s, a, a, s.B)) return rc;
+  const bool vec = s.D % 4 == 0 && !desc->delta_broadcast && reinterpret_cast<uintptr_t>(a.u) % (4 * sizeof(T)) == 0 &&
+                   reinterpret_cast<uintptr_t>(a.delta) % (4 * sizeof(T)) == 0;
   if (!dispatch_spl<4, 8>(s.spl_f, s.epi, [&](auto spl, auto epi) {
         constexpr int S = decltype(spl)::value;
         constexpr bool E = decltype(epi)::value;
         auto go = [&](auto sp) {
           constexpr bool SP = decltype(sp)::value;
-          if (s.nseg > 1)  // aggregates of every segment but the last
-            hipLaunchKernelGGL((ssm_fwd_agg_kernel<S, SP, T>), dim3(s.ncb, s.B, s.nseg - 1),
-                               dim3(kWave * kFwdWaves), 0, st, a);
           if (vec)
             hipLaunchKernelGGL((ssm_fwd_kernel<S, E, SP, true, T>), dim3(s.ncb, s.B, s.nseg),
                                dim3(kWave * kFwdWaves), 0, st, a);
@@ -1499,10 +1540,9 @@ int launch_fwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const voi
 }
 
 template <typename T>
-int launch_bwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const void* u, const void* delta,
-               const float* A, const void* Bc, const void* Cc, const float* Dskip, const void* z,
-               const float* ckpt, const void* dy, void* du, void* ddelta, float* dA, void* dB, void* dC,
-               float* dD, void* dz, void* workspace) {
+BwdArgs<T> bwd_args(const ssm_desc_t* desc, const Shape& s, const void* u, const void* delta, const float* A,
+                    const void* Bc, const void* Cc, const float* Dskip, const void* z, const float* ckpt,
+                    const void* dy, void* du, void* ddelta, void* dz, void* workspace) {
   const bool bcast = desc->delta_broadcast != 0;
   const WsLayout wl = ws_layout(s, bcast);
   float* ws = static_cast<float*>(workspace);
@@ -1538,12 +1578,34 @@ int launch_bwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const voi
   a.ldz = s.ldz;
   a.dstride = bcast ? 0 : 1;
   a.flags = desc->flags;
+  return a;
+}
+
+// Adjoint aggregates of every segment but the first (s.nseg > 1): rows of a0,
+// and with a pair (rows = 2 * s.B) the rows of a1 in the same launch.
+template <typename T>
+int launch_bwd_agg(hipStream_t st, const Shape& s, const BwdArgs<T>& a0, const BwdArgs<T>& a1, int rows) {
   if (!dispatch_spl<2, 4>(s.spl_b, s.epi, [&](auto spl, auto epi) {
         constexpr int S = decltype(spl)::value;
         constexpr bool E = decltype(epi)::value;
-        if (s.nseg > 1)  // adjoint aggregates of every segment but the first
-          hipLaunchKernelGGL((ssm_bwd_agg_kernel<S, E, T>), dim3(s.ncb, s.B, s.nseg - 1), dim3(kWave * kBwdWaves),
-                             0, st, a);
+        hipLaunchKernelGGL((ssm_bwd_agg_kernel<S, E, T>), dim3(s.ncb, rows, s.nseg - 1), dim3(kWave * kBwdWaves), 0,
+                           st, a0, a1, s.B);
+      }))
+    return fail(SSM_ERR_UNSUPPORTED, "no kernel variant for this shape");
+  return hip_check(hipGetLastError(), "ssm_bwd aggregate launch");
+}
+
+template <typename T>
+int launch_bwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const BwdArgs<T>& a, float* dA, void* dB,
+               void* dC, float* dD, void* ddelta, void* workspace, bool with_agg) {
+  const bool bcast = desc->delta_broadcast != 0;
+  const WsLayout wl = ws_layout(s, bcast);
+  float* ws = static_cast<float*>(workspace);
+  if (with_agg && s.nseg > 1)
+    if (int rc = launch_bwd_agg<T>(st, s, a, a, s.B)) return rc;
+  if (!dispatch_spl<2, 4>(s.spl_b, s.epi, [&](auto spl, auto epi) {
+        constexpr int S = decltype(spl)::value;
+        constexpr bool E = decltype(epi)::value;
         if (desc->delta_broadcast)
           hipLaunchKernelGGL((ssm_bwd_kernel<S, E, true, T>), dim3(s.ncb, s.B, s.nseg), dim3(kWave * kBwdWaves), 0,
                              st, a);
@@ -1633,8 +1695,10 @@ int ssm_fwd(void* stream, const ssm_desc_t* desc, const void* u, const void* del
   if ((desc->flags & SSM_GATE) && !z) return fail(SSM_ERR_INVALID, "SSM_GATE needs z");
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (desc->dtype == SSM_F32)
-    return launch_fwd<float>(st, desc, s, u, delta, A, Bc, Cc, Dskip, z, y, ckpt, workspace);
-  return launch_fwd<bf16>(st, desc, s, u, delta, A, Bc, Cc, Dskip, z, y, ckpt, workspace);
+    return launch_fwd<float>(st, desc, s, fwd_args<float>(desc, s, u, delta, A, Bc, Cc, Dskip, z, y, ckpt, workspace),
+                             true);
+  return launch_fwd<bf16>(st, desc, s, fwd_args<bf16>(desc, s, u, delta, A, Bc, Cc, Dskip, z, y, ckpt, workspace),
+                          true);
 }
 
 int ssm_bwd(void* stream, const ssm_desc_t* desc, const void* u, const void* delta, const float* A,
@@ -1649,10 +1713,85 @@ int ssm_bwd(void* stream, const ssm_desc_t* desc, const void* u, const void* del
   if ((desc->flags & SSM_GATE) && (!z || !dz)) return fail(SSM_ERR_INVALID, "SSM_GATE needs z and dz");
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (desc->dtype == SSM_F32)
-    return launch_bwd<float>(st, desc, s, u, delta, A, Bc, Cc, Dskip, z, ckpt, dy, du, ddelta, dA, dB, dC, dD,
-                             dz, workspace);
-  return launch_bwd<bf16>(st, desc, s, u, delta, A, Bc, Cc, Dskip, z, ckpt, dy, du, ddelta, dA, dB, dC, dD, dz,
-                          workspace);
+    return launch_bwd<float>(st, desc, s,
+                             bwd_args<float>(desc, s, u, delta, A, Bc, Cc, Dskip, z, ckpt, dy, du, ddelta, dz, workspace),
+                             dA, dB, dC, dD, ddelta, workspace, true);
+  return launch_bwd<bf16>(st, desc, s,
+                          bwd_args<bf16>(desc, s, u, delta, A, Bc, Cc, Dskip, z, ckpt, dy, du, ddelta, dz, workspace),
+                          dA, dB, dC, dD, ddelta, workspace, true);
+}
+
+// The two calls of a pair as ssm_fwd / ssm_bwd would make them, with the
+// time-split aggregate passes of both in one launch when the two descs have
+// the same shape and kernel variant (each keeps its own segments, so the
+// results equal two separate calls bit for bit).
+static bool same_shape(const ssm_desc_t& a, const ssm_desc_t& b) {
+  return a.batch == b.batch && a.seqlen == b.seqlen && a.dim == b.dim && a.dstate == b.dstate &&
+         a.dtype == b.dtype && a.delta_broadcast == b.delta_broadcast && a.segments == b.segments &&
+         ((a.flags ^ b.flags) & SSM_DELTA_SOFTPLUS) == 0;
+}
+
+int ssm_fwd_pair(void* stream, const ssm_desc_t* desc, const ssm_fwd_io_t* io) {
+  g_last_error.clear();
+  if (desc == nullptr || io == nullptr) return fail(SSM_ERR_INVALID, "ssm_fwd_pair: desc or io is NULL");
+  Shape s[2];
+  for (int k = 0; k < 2; ++k) {
+    if (int rc = validate(&desc[k], &s[k])) return rc;
+    const ssm_fwd_io_t& q = io[k];
+    if (!q.u || !q.delta || !q.A || !q.B || !q.C || !q.y)
+      return fail(SSM_ERR_INVALID, "ssm_fwd_pair: required pointer is NULL");
+    if (s[k].nseg > 1 && !q.workspace)
+      return fail(SSM_ERR_INVALID, "ssm_fwd_pair: workspace is NULL but ssm_fwd_workspace_bytes > 0");
+    if ((desc[k].flags & SSM_SKIP) && !q.D) return fail(SSM_ERR_INVALID, "SSM_SKIP needs D");
+    if ((desc[k].flags & SSM_GATE) && !q.z) return fail(SSM_ERR_INVALID, "SSM_GATE needs z");
+  }
+  const bool joint = same_shape(desc[0], desc[1]) && s[0].nseg > 1;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  auto run = [&](auto tag) -> int {
+    using T = decltype(tag);
+    FwdArgs<T> a[2];
+    for (int k = 0; k < 2; ++k)
+      a[k] = fwd_args<T>(&desc[k], s[k], io[k].u, io[k].delta, io[k].A, io[k].B, io[k].C, io[k].D, io[k].z,
+                         io[k].y, io[k].ckpt, io[k].workspace);
+    if (joint)
+      if (int rc = launch_fwd_agg<T>(st, s[0], a[0], a[1], 2 * s[0].B)) return rc;
+    for (int k = 0; k < 2; ++k)
+      if (int rc = launch_fwd<T>(st, &desc[k], s[k], a[k], !joint)) return rc;
+    return SSM_OK;
+  };
+  return desc[0].dtype == SSM_F32 ? run(float{}) : run(bf16{});
+}
+
+int ssm_bwd_pair(void* stream, const ssm_desc_t* desc, const ssm_bwd_io_t* io) {
+  g_last_error.clear();
+  if (desc == nullptr || io == nullptr) return fail(SSM_ERR_INVALID, "ssm_bwd_pair: desc or io is NULL");
+  Shape s[2];
+  for (int k = 0; k < 2; ++k) {
+    if (int rc = validate(&desc[k], &s[k])) return rc;
+    const ssm_bwd_io_t& q = io[k];
+    if (!q.u || !q.delta || !q.A || !q.B || !q.C || !q.ckpt || !q.dy || !q.du || !q.ddelta || !q.dA || !q.dB ||
+        !q.dC || !q.workspace)
+      return fail(SSM_ERR_INVALID, "ssm_bwd_pair: required pointer is NULL");
+    if ((desc[k].flags & SSM_SKIP) && (!q.D || !q.dD)) return fail(SSM_ERR_INVALID, "SSM_SKIP needs D and dD");
+    if ((desc[k].flags & SSM_GATE) && (!q.z || !q.dz)) return fail(SSM_ERR_INVALID, "SSM_GATE needs z and dz");
+  }
+  const bool joint = same_shape(desc[0], desc[1]) && s[0].nseg > 1 && s[0].epi == s[1].epi;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  auto run = [&](auto tag) -> int {
+    using T = decltype(tag);
+    BwdArgs<T> a[2];
+    for (int k = 0; k < 2; ++k)
+      a[k] = bwd_args<T>(&desc[k], s[k], io[k].u, io[k].delta, io[k].A, io[k].B, io[k].C, io[k].D, io[k].z,
+                         io[k].ckpt, io[k].dy, io[k].du, io[k].ddelta, io[k].dz, io[k].workspace);
+    if (joint)
+      if (int rc = launch_bwd_agg<T>(st, s[0], a[0], a[1], 2 * s[0].B)) return rc;
+    for (int k = 0; k < 2; ++k)
+      if (int rc = launch_bwd<T>(st, &desc[k], s[k], a[k], io[k].dA, io[k].dB, io[k].dC, io[k].dD, io[k].ddelta,
+                                 io[k].workspace, !joint))
+        return rc;
+    return SSM_OK;
+  };
+  return desc[0].dtype == SSM_F32 ? run(float{}) : run(bf16{});
 }
 
 }  // extern "C"

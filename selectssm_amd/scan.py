@@ -192,6 +192,63 @@ def scan_bwd(u, delta, A, B, C, Dskip, z, ckpt, dy, reverse=False, complement=Fa
     return du, ddelta, dA, dB, dC, dD, dz
 
 
+def scan_fwd_pair(calls):
+    """Run ``ssm_fwd_pair``: two :func:`scan_fwd` calls, given as dicts of its
+    keyword arguments, with the time-split aggregate passes of both in one
+    launch where their shapes allow (results equal the two calls bit for bit).
+    Returns ``[(y, ckpt), (y, ckpt)]``."""
+    if len(calls) != 2:
+        raise ValueError("scan_fwd_pair takes two calls")
+    lib = L.lib()
+    descs, ios, outs = (L.SsmDesc * 2)(), (L.SsmFwdIo * 2)(), []
+    for k, c in enumerate(calls):
+        u, delta, A, B, C = c["u"], c["delta"], c["A"], c["B"], c["C"]
+        Dskip, z = c.get("Dskip"), c.get("z")
+        flags = _flags(Dskip is not None, z is not None, c.get("reverse", False), c.get("complement", False),
+                       c.get("delta_softplus", False))
+        y = torch.empty_like(u) if c.get("y_out") is None else c["y_out"]
+        ld_y, ld_z = row_stride(y), (row_stride(z) if z is not None else 0)
+        if ld_y is None or ld_z is None:
+            raise ValueError("y_out and z must be contiguous or column slices of a contiguous (B, L, W) tensor")
+        descs[k] = _desc(u, delta, A, flags, c.get("segments", 0), ld_y=ld_y, ld_z=ld_z)
+        ckpt = (_scratch(L.size_query(lib.ssm_ckpt_bytes, descs[k]), u.device) if c.get("want_ckpt", True)
+                else None)
+        ws = _scratch(L.size_query(lib.ssm_fwd_workspace_bytes, descs[k], allow_zero=True), u.device)
+        ios[k] = L.SsmFwdIo(_ptr(u), _ptr(delta), _ptr(A), _ptr(B), _ptr(C), _ptr(Dskip), _ptr(z), _ptr(y),
+                            _ptr(ckpt), _ptr(ws))
+        outs.append((y, ckpt, ws))
+    L.check(lib.ssm_fwd_pair(_stream(), descs, ios))
+    return [(y, ckpt) for y, ckpt, _ in outs]
+
+
+def scan_bwd_pair(calls):
+    """Run ``ssm_bwd_pair``: two :func:`scan_bwd` calls, given as dicts of its
+    keyword arguments (``u, delta, A, B, C, Dskip, z, ckpt, dy`` and the flags).
+    Returns the two ``(du, ddelta, dA, dB, dC, dD, dz)`` tuples."""
+    if len(calls) != 2:
+        raise ValueError("scan_bwd_pair takes two calls")
+    lib = L.lib()
+    descs, ios, outs = (L.SsmDesc * 2)(), (L.SsmBwdIo * 2)(), []
+    for k, c in enumerate(calls):
+        u, delta, A, B, C, dy = c["u"], c["delta"], c["A"], c["B"], c["C"], c["dy"]
+        Dskip, z = c.get("Dskip"), c.get("z")
+        flags = _flags(Dskip is not None, z is not None, c.get("reverse", False), c.get("complement", False),
+                       c.get("delta_softplus", False))
+        ld_y, ld_z = row_stride(dy), (row_stride(z) if z is not None else 0)
+        if ld_y is None or ld_z is None:
+            raise ValueError("dy and z must be contiguous or column slices of a contiguous (B, L, W) tensor")
+        descs[k] = _desc(u, delta, A, flags, c.get("segments", 0), ld_y=ld_y, ld_z=ld_z)
+        g = (torch.empty_like(u), torch.empty_like(delta), torch.empty_like(A), torch.empty_like(B),
+             torch.empty_like(C), torch.empty_like(Dskip) if Dskip is not None else None,
+             torch.empty_like(z) if z is not None else None)
+        ws = _scratch(L.size_query(lib.ssm_bwd_workspace_bytes, descs[k]), u.device)
+        ios[k] = L.SsmBwdIo(_ptr(u), _ptr(delta), _ptr(A), _ptr(B), _ptr(C), _ptr(Dskip), _ptr(z), _ptr(c["ckpt"]),
+                            _ptr(dy), *(_ptr(t) for t in g), _ptr(ws))
+        outs.append((g, ws))
+    L.check(lib.ssm_bwd_pair(_stream(), descs, ios))
+    return [g for g, _ in outs]
+
+
 # ------------------------------------------------------------------- autograd
 
 class SelectiveScanFn(torch.autograd.Function):

@@ -135,3 +135,23 @@ def test_conv_desc_validation():
     assert lib.ssm_conv_fwd(None, ctypes.byref(d), None, p, p) == L.SSM_ERR_INVALID
     assert lib.ssm_conv_bwd(None, ctypes.byref(d), p, p, p, p, p, None) == L.SSM_ERR_INVALID
     assert b"workspace" in lib.ssm_last_error()
+
+
+def test_pair_entry_points_validate_before_launching():
+    """ssm_fwd_pair / ssm_bwd_pair reject missing arrays and invalid descs without touching a GPU."""
+    lib = L.lib()
+    assert lib.ssm_fwd_pair(None, None, None) == L.SSM_ERR_INVALID
+    assert lib.ssm_bwd_pair(None, None, None) == L.SSM_ERR_INVALID
+    good = L.make_desc(2, 64, 64, 16)
+    bad = L.make_desc(2, 64, 64, 64)  # dstate beyond 32
+    descs = (L.SsmDesc * 2)(good, bad)
+    p = ctypes.c_void_p(16)
+    fio = (L.SsmFwdIo * 2)(*[L.SsmFwdIo(p, p, p, p, p, None, None, p, None, None)] * 2)
+    assert lib.ssm_fwd_pair(None, descs, fio) == L.SSM_ERR_INVALID
+    assert b"dstate" in lib.ssm_last_error()
+    descs = (L.SsmDesc * 2)(good, good)
+    fio[1].y = None
+    assert lib.ssm_fwd_pair(None, descs, fio) == L.SSM_ERR_INVALID
+    assert b"NULL" in lib.ssm_last_error()
+    bio = (L.SsmBwdIo * 2)()
+    assert lib.ssm_bwd_pair(None, descs, bio) == L.SSM_ERR_INVALID
