@@ -206,7 +206,7 @@ def main():
         print(json.dumps(module_bench(args)), flush=True)
         return
 
-    from selectssm_amd.scan import scan_bwd, scan_fwd
+    from selectssm_amd.scan import scan_bwd, scan_bwd_pair, scan_fwd, scan_fwd_pair
     from selectssm_amd.synthetic import make_inputs_gpu
 
     cfg = CONFIGS[args.config]
@@ -223,35 +223,43 @@ def main():
     if cfg["directions"] == 2:
         dirs.append(dict(A=(A * 0.5).contiguous(), reverse=True, complement=True))
 
-    def fwd(dr):
-        return scan_fwd(u, dt, dr["A"], Bc, Cc, None, z, dr["reverse"], dr["complement"])
+    def call(dr):
+        return dict(u=u, delta=dt, A=dr["A"], B=Bc, C=Cc, z=z, reverse=dr["reverse"], complement=dr["complement"])
 
-    def bwd(dr, ckpt):
-        return scan_bwd(u, dt, dr["A"], Bc, Cc, None, z, ckpt, g, dr["reverse"], dr["complement"])
+    # one direction: ssm_fwd then ssm_bwd; two: ssm_fwd_pair then
+    # ssm_bwd_pair, whose time-split aggregate passes cover both directions
+    def fwd():
+        if len(dirs) == 2:
+            return [ck for _, ck in scan_fwd_pair([call(dr) for dr in dirs])]
+        return [scan_fwd(u, dt, A, Bc, Cc, None, z)[1]]
+
+    def bwd(cks):
+        if len(dirs) == 2:
+            return scan_bwd_pair([dict(call(dr), ckpt=ck, dy=g) for dr, ck in zip(dirs, cks)])
+        return scan_bwd(u, dt, A, Bc, Cc, None, z, cks[0], g)
 
     for _ in range(args.warmup):
-        for dr in dirs:
-            bwd(dr, fwd(dr)[1])
+        bwd(fwd())
     torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats()
 
     K = args.steps
     nd = len(dirs)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3 * nd)] for _ in range(K)]
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(K)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for k in range(K):
-        for i, dr in enumerate(dirs):
-            ev[k][3 * i].record()
-            y, ckpt = fwd(dr)
-            ev[k][3 * i + 1].record()
-            bwd(dr, ckpt)
-            ev[k][3 * i + 2].record()
+        ev[k][0].record()
+        cks = fwd()
+        ev[k][1].record()
+        bwd(cks)
+        ev[k][2].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
 
-    fwd_ms = sum(e[3 * i].elapsed_time(e[3 * i + 1]) for e in ev for i in range(nd)) / (K * nd)
-    bwd_ms = sum(e[3 * i + 1].elapsed_time(e[3 * i + 2]) for e in ev for i in range(nd)) / (K * nd)
+    # per direction (a pair call's time split evenly between its two scans)
+    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / (K * nd)
+    bwd_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / (K * nd)
     fwd_b, bwd_b = alg_bytes(B, L, D, N, w, gate=args.gate)
     tokens = B * L * K
     achieved = bwd_b / (bwd_ms * 1e-3) / 1e9

@@ -10,9 +10,10 @@ The hot path is fused:
   * flip + ``shift_conv`` + activation  -> one ``ssm_conv_fwd`` launch
   * softplus(dt), the scan, the un-flip, the D skip (with the reference's
     flipped-domain ``u``), and in BidirectionalMamba the silu gate
-                                        -> one ``ssm_fwd`` launch per direction,
-    both writing straight into the concatenated output; the conv inputs and the
-    gates are read in place from in_proj's output
+                                        -> one ``ssm_fwd`` per direction, the two
+    as one ``ssm_fwd_pair`` call (their time-split aggregate passes share a
+    launch), both writing straight into the concatenated output; the conv
+    inputs and the gates are read in place from in_proj's output
   * the Dense projections (BC, dt, dt_proj, in_proj, out_proj) run on hipBLASLt
     through torch.
 Every strategy flag (chunked / ``recursive_scan`` / ``custom_vjp_scan``) runs the
@@ -31,8 +32,8 @@ import torch
 import torch.nn.functional as F
 
 from .conv import conv1d_act
-from .scan import (_check_recursion, as_rows, bidirectional_selective_scan, resolve_chunking, scan_bwd, scan_fwd,
-                   selective_scan)
+from .scan import (_check_recursion, as_rows, bidirectional_selective_scan, resolve_chunking, scan_bwd,
+                   scan_bwd_pair, scan_fwd, scan_fwd_pair, selective_scan)
 
 _FUSED_CONV_ACTS = ("silu", "relu", None)
 
@@ -173,8 +174,9 @@ def _tn(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     return torch.bmm(b3.transpose(1, 2), a3).sum(0).t()
 
 
-def _core_forward(u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, Dp, z, N, rank, reverse, complement, y_out=None):
-    """Projections + scan (selectssm.py:190-238); returns (y, saved tensors)."""
+def _core_project(u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, N, rank):
+    """The scan's operands from u (selectssm.py:190-210): (A, dt_low, dt, B, C),
+    dt before its softplus, which the scan applies."""
     B_, L_, D = u.shape
     u2 = u.reshape(-1, D)
     BC = torch.addmm(bbc.to(u.dtype), u2, Wbc.to(u.dtype))
@@ -188,16 +190,35 @@ def _core_forward(u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, Dp, z, N, rank, reverse,
     Bc = BC[:, :N].reshape(B_, L_, N).contiguous()
     Cc = BC[:, N:].reshape(B_, L_, N).contiguous()
     A = -torch.exp(A_log)
-    y, ckpt = scan_fwd(u, dt.contiguous(), A, Bc, Cc, Dp, z, reverse, complement, delta_softplus=True, y_out=y_out)
+    return A, dt_low, dt.contiguous(), Bc, Cc
+
+
+def _core_forward(u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, Dp, z, N, rank, reverse, complement, y_out=None):
+    """Projections + scan (selectssm.py:190-238); returns (y, saved tensors)."""
+    A, dt_low, dt, Bc, Cc = _core_project(u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, N, rank)
+    y, ckpt = scan_fwd(u, dt, A, Bc, Cc, Dp, z, reverse, complement, delta_softplus=True, y_out=y_out)
     return y, (u, A, Wbc, Wdt, Wp, Dp, z, dt_low, dt, Bc, Cc, ckpt)
+
+
+def _scan_call(saved, reverse, complement):
+    """The scan's arguments for the scan_*_pair launchers, from _core_forward's saved tensors."""
+    u, A, _, _, _, Dp, z, _, dt, Bc, Cc, ckpt = saved
+    return dict(u=u, delta=dt, A=A, B=Bc, C=Cc, Dskip=Dp, z=z, reverse=reverse, complement=complement,
+                delta_softplus=True)
 
 
 def _core_backward(saved, dy, N, rank, reverse, complement):
     """Gradients of _core_forward for (u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, D, z)."""
     u, A, Wbc, Wdt, Wp, Dp, z, dt_low, dt, Bc, Cc, ckpt = saved
+    grads = scan_bwd(u, dt, A, Bc, Cc, Dp, z, ckpt, dy, reverse, complement, delta_softplus=True)
+    return _core_param_grads(saved, grads, N, rank)
+
+
+def _core_param_grads(saved, grads, N, rank):
+    """_core_backward after the scan's backward: the projections' and u's gradients."""
+    u, A, Wbc, Wdt, Wp, Dp, z, dt_low, dt, Bc, Cc, ckpt = saved
+    du, ddt, dA, dB, dC, dD, dz = grads
     D = u.shape[-1]
-    du, ddt, dA, dB, dC, dD, dz = scan_bwd(u, dt.contiguous(), A, Bc, Cc, Dp, z, ckpt, dy, reverse, complement,
-                                           delta_softplus=True)
     u2 = u.reshape(-1, D)
     du2 = du.reshape(-1, D)
     dBC = torch.cat([dB.reshape(-1, N), dC.reshape(-1, N)], dim=1)
@@ -273,10 +294,16 @@ class _PairCoreFn(torch.autograd.Function):
                 ur, A_logr, Wbcr, bbcr, Wdtr, bdtr, Wpr, bpr, Dr, zr, N, rank, complement):
         B_, L_, E = uf.shape
         y = torch.empty(B_, L_, 2 * E, dtype=uf.dtype, device=uf.device)
-        _, sf = _core_forward(uf, A_logf, Wbcf, bbcf, Wdtf, bdtf, Wpf, bpf, Df, zf, N, rank, False, False,
-                              y_out=y[..., :E])
-        _, sr = _core_forward(ur, A_logr, Wbcr, bbcr, Wdtr, bdtr, Wpr, bpr, Dr, zr, N, rank, True, complement,
-                              y_out=y[..., E:])
+        pf = _core_project(uf, A_logf, Wbcf, bbcf, Wdtf, bdtf, Wpf, bpf, N, rank)
+        pr = _core_project(ur, A_logr, Wbcr, bbcr, Wdtr, bdtr, Wpr, bpr, N, rank)
+        # both directions' scans in one pair call (their time-split aggregate passes share a launch)
+        calls = [dict(u=u, delta=p[2], A=p[0], B=p[3], C=p[4], Dskip=Dp, z=z, reverse=rev, complement=comp,
+                      delta_softplus=True, y_out=yo)
+                 for u, p, Dp, z, rev, comp, yo in ((uf, pf, Df, zf, False, False, y[..., :E]),
+                                                    (ur, pr, Dr, zr, True, complement, y[..., E:]))]
+        (_, ckf), (_, ckr) = scan_fwd_pair(calls)
+        sf = (uf, pf[0], Wbcf, Wdtf, Wpf, Df, zf, pf[1], pf[2], pf[3], pf[4], ckf)
+        sr = (ur, pr[0], Wbcr, Wdtr, Wpr, Dr, zr, pr[1], pr[2], pr[3], pr[4], ckr)
         ctx.save_for_backward(*sf, *sr)
         ctx.cfg = (N, rank, complement, len(sf))
         return y
@@ -287,8 +314,11 @@ class _PairCoreFn(torch.autograd.Function):
         saved = ctx.saved_tensors
         E = saved[0].shape[-1]
         dy, _ = as_rows(dy, saved[0].dtype)
-        gf = _core_backward(saved[:k], dy[..., :E], N, rank, False, False)
-        gr = _core_backward(saved[k:], dy[..., E:], N, rank, True, complement)
+        sf, sr = saved[:k], saved[k:]
+        scan_gf, scan_gr = scan_bwd_pair([dict(_scan_call(sf, False, False), ckpt=sf[-1], dy=dy[..., :E]),
+                                          dict(_scan_call(sr, True, complement), ckpt=sr[-1], dy=dy[..., E:])])
+        gf = _core_param_grads(sf, scan_gf, N, rank)
+        gr = _core_param_grads(sr, scan_gr, N, rank)
         return (*gf, *gr, None, None, None)
 
 

@@ -319,10 +319,12 @@ class BidirectionalScanFn(torch.autograd.Function):
         Bt, Ln, D = uf.shape
         y = torch.empty(Bt, Ln, 2 * D, dtype=uf.dtype, device=uf.device)
         want = torch.is_grad_enabled() or any(ctx.needs_input_grad)
-        _, ckf = scan_fwd(uf, dtf, Af, Bf, Cf, Df, zf, False, False, want_ckpt=want, delta_softplus=delta_softplus,
-                          y_out=y[..., :D])
-        _, ckr = scan_fwd(ur, dtr, Ar, Br, Cr, Dr, zr, True, complement, want_ckpt=want,
-                          delta_softplus=delta_softplus, y_out=y[..., D:])
+        # one pair call: the time-split aggregate passes of both directions share a launch
+        (_, ckf), (_, ckr) = scan_fwd_pair([
+            dict(u=uf, delta=dtf, A=Af, B=Bf, C=Cf, Dskip=Df, z=zf, want_ckpt=want, delta_softplus=delta_softplus,
+                 y_out=y[..., :D]),
+            dict(u=ur, delta=dtr, A=Ar, B=Br, C=Cr, Dskip=Dr, z=zr, reverse=True, complement=complement,
+                 want_ckpt=want, delta_softplus=delta_softplus, y_out=y[..., D:])])
         ctx.save_for_backward(uf, dtf, Af, Bf, Cf, Df, zf, ckf, ur, dtr, Ar, Br, Cr, Dr, zr, ckr)
         ctx.cfg = (complement, delta_softplus)
         return y
@@ -333,8 +335,10 @@ class BidirectionalScanFn(torch.autograd.Function):
         complement, dsp = ctx.cfg
         D = uf.shape[-1]
         dy, _ = as_rows(dy, uf.dtype)
-        gf = scan_bwd(uf, dtf, Af, Bf, Cf, Df, zf, ckf, dy[..., :D], False, False, delta_softplus=dsp)
-        gr = scan_bwd(ur, dtr, Ar, Br, Cr, Dr, zr, ckr, dy[..., D:], True, complement, delta_softplus=dsp)
+        gf, gr = scan_bwd_pair([
+            dict(u=uf, delta=dtf, A=Af, B=Bf, C=Cf, Dskip=Df, z=zf, ckpt=ckf, dy=dy[..., :D], delta_softplus=dsp),
+            dict(u=ur, delta=dtr, A=Ar, B=Br, C=Cr, Dskip=Dr, z=zr, ckpt=ckr, dy=dy[..., D:], reverse=True,
+                 complement=complement, delta_softplus=dsp)])
         return (*gf, *gr, None, None)
 
 
