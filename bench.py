@@ -69,15 +69,15 @@ def read_traffic(path):
         return None
 
 
-def cpu_baseline(B, L, D, N):
-    """Time the C port of the reference's custom-VJP path on a sample: half the batch rows."""
+def cpu_baseline(B, L, D, N, tensors):
+    """Time the C port of the reference's custom-VJP path on a sample: half the batch
+    rows of the very arrays the GPU ran (``tensors``: u, dt, A, B, C, g on the GPU)."""
     import numpy as np
     from oracle import c_oracle
-    from selectssm_amd.synthetic import make_inputs
 
     cores = len(os.sched_getaffinity(0))
     sb = min(4, B)  # 4 of the 8 batch rows: about 3 s per run on 16 cores, 10-15 s in all
-    inp = make_inputs(sb, L, D, N, seed=0)
+    inp = {k: (t if k == "A" else t[:sb]).float().cpu().numpy() for k, t in tensors.items()}
     args = (inp["u"], inp["dt"], inp["A"], inp["B"], inp["C"])
     times = []
     for rep in range(4):  # first run is the warmup
@@ -91,7 +91,8 @@ def cpu_baseline(B, L, D, N):
         "unit": "tokens/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"fwd+bwd of batch rows {sb} of {B} (L={L}, D={D}, N={N}, fp32), recursive custom-VJP "
+        "sample": f"fwd+bwd of batch rows 0..{sb - 1} of {B} of the GPU run's inputs (L={L}, D={D}, N={N}, "
+                  f"fp32), recursive custom-VJP "
                   f"algorithm (min_recursion_length=2, recursive_split=2), median of 3 after 1 warmup, "
                   f"{t:.2f} s per run",
     }
@@ -301,7 +302,7 @@ def main():
         "peak_hbm_bytes": torch.cuda.max_memory_allocated(),
     }
     if not args.no_cpu_baseline and args.config == 1 and not args.gate:
-        line["cpu_baseline"] = cpu_baseline(B, L, D, N)
+        line["cpu_baseline"] = cpu_baseline(B, L, D, N, dict(u=u, dt=dt, A=A, B=Bc, C=Cc, g=g))
     print(json.dumps(line), flush=True)
 
 

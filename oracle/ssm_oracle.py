@@ -33,9 +33,18 @@ Pinning (what checks each function, in ``tests/test_oracle.py``):
                           the reverse map and skip quirk checked as an identity
                           between the reverse module and the forward module on
                           the flipped input; reduces to scan_forward + skip for
-                          a unit 1-tap conv, no activation and identity dt
-  bidirectional_mamba_forward  composition of selectssm.py:282-364; split /
-                          tie / concat checked against explicit slicing
+                          a unit 1-tap conv, no activation and identity dt;
+                          the dt_proj branch equals one Dense with the composed
+                          kernel (non-square and square non-symmetric dt_proj)
+  bidirectional_mamba_forward  composition of selectssm.py:282-364, checked
+                          against an expected output assembled from separately
+                          drawn in_proj column blocks (every tie_in_proj /
+                          tie_gate combination, concat and sum, rms and layer
+                          norm, the MLP); dt_rank from the block's input width
+  rms_norm, layer_norm    closed forms on constant and sign-alternating rows;
+                          torch's fp64 rms_norm / layer_norm
+  gelu_tanh               gelu(x) - gelu(-x) = x, asymptotes, torch's fp64
+                          tanh-approximate gelu
   ssm_block_forward/_bwd  explicit np.flip composition; finite differences
 """
 from __future__ import annotations
@@ -303,8 +312,8 @@ def conv1d_silu_backward(x, w, du):
 
 def gelu_tanh(x):
     """0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))): flax.linen.gelu's default
-    (approximate=True).  That default lives in Flax, not in the reference:
-    parity unpinned beyond this closed form."""
+    (approximate=True).  The closed form is pinned (identities, torch); that
+    Flax's default is the tanh form lives in Flax, not in the reference (unpinned)."""
     x = np.asarray(x, np.float64)
     return 0.5 * x * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (x + 0.044715 * x ** 3)))
 
@@ -392,13 +401,15 @@ def selective_ssm_forward(p, x, reverse=False, complement=False, hidden_features
 
 
 def rms_norm(x, scale, eps=1e-6):
-    """flax.linen.RMSNorm (epsilon default 1e-6: a Flax default, parity unpinned)."""
+    """flax.linen.RMSNorm.  The formula is pinned (closed forms, torch); the epsilon
+    1e-6 is Flax's default, which the reference leaves implicit (unpinned)."""
     x = np.asarray(x, np.float64)
     return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps) * np.asarray(scale, np.float64)
 
 
 def layer_norm(x, scale, bias, eps=1e-6):
-    """flax.linen.LayerNorm (epsilon default 1e-6: a Flax default, parity unpinned)."""
+    """flax.linen.LayerNorm.  The formula is pinned (closed forms, torch); the epsilon
+    1e-6 is Flax's default, which the reference leaves implicit (unpinned)."""
     x = np.asarray(x, np.float64)
     m = x.mean(-1, keepdims=True)
     v = ((x - m) ** 2).mean(-1, keepdims=True)

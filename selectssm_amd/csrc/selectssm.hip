@@ -1373,6 +1373,7 @@ struct Shape {
 // kMinAutoSeg steps long.  The choice depends on the desc alone, so a given
 // desc always computes in the same order.
 constexpr int kFillWaves = 2048;
+constexpr int kMaxGridY = 65535;  // grid.y limit: batch rows (or both calls' rows of a pair) per launch
 constexpr int kMinAutoSeg = 512;
 constexpr int kMaxSeg = 1024;
 
@@ -1394,7 +1395,7 @@ int validate(const ssm_desc_t* desc, Shape* s) {
   if (desc->batch < 1 || desc->seqlen < 1 || desc->dim < 1)
     return fail(SSM_ERR_INVALID, "batch, seqlen and dim must be >= 1");
   if (desc->dstate < 1 || desc->dstate > 32) return fail(SSM_ERR_INVALID, "dstate must be in 1..32");
-  if (desc->batch > 65535) return fail(SSM_ERR_INVALID, "batch must be <= 65535");
+  if (desc->batch > kMaxGridY) return fail(SSM_ERR_INVALID, "batch must be <= 65535");
   // per-batch-row byte offsets are 32-bit inside the kernels
   if (desc->seqlen * desc->dim > (int64_t(1) << 30) || desc->seqlen * desc->dstate > (int64_t(1) << 30))
     return fail(SSM_ERR_INVALID, "seqlen*dim and seqlen*dstate must be <= 2^30");
@@ -1745,7 +1746,9 @@ int ssm_fwd_pair(void* stream, const ssm_desc_t* desc, const ssm_fwd_io_t* io) {
     if ((desc[k].flags & SSM_SKIP) && !q.D) return fail(SSM_ERR_INVALID, "SSM_SKIP needs D");
     if ((desc[k].flags & SSM_GATE) && !q.z) return fail(SSM_ERR_INVALID, "SSM_GATE needs z");
   }
-  const bool joint = same_shape(desc[0], desc[1]) && s[0].nseg > 1;
+  // one element type for both calls: the kernels of a pair are chosen once
+  if (desc[0].dtype != desc[1].dtype) return fail(SSM_ERR_INVALID, "ssm_fwd_pair: the two descs must have the same dtype");
+  const bool joint = same_shape(desc[0], desc[1]) && s[0].nseg > 1 && 2 * s[0].B <= kMaxGridY;
   hipStream_t st = static_cast<hipStream_t>(stream);
   auto run = [&](auto tag) -> int {
     using T = decltype(tag);
@@ -1775,7 +1778,8 @@ int ssm_bwd_pair(void* stream, const ssm_desc_t* desc, const ssm_bwd_io_t* io) {
     if ((desc[k].flags & SSM_SKIP) && (!q.D || !q.dD)) return fail(SSM_ERR_INVALID, "SSM_SKIP needs D and dD");
     if ((desc[k].flags & SSM_GATE) && (!q.z || !q.dz)) return fail(SSM_ERR_INVALID, "SSM_GATE needs z and dz");
   }
-  const bool joint = same_shape(desc[0], desc[1]) && s[0].nseg > 1 && s[0].epi == s[1].epi;
+  if (desc[0].dtype != desc[1].dtype) return fail(SSM_ERR_INVALID, "ssm_bwd_pair: the two descs must have the same dtype");
+  const bool joint = same_shape(desc[0], desc[1]) && s[0].nseg > 1 && s[0].epi == s[1].epi && 2 * s[0].B <= kMaxGridY;
   hipStream_t st = static_cast<hipStream_t>(stream);
   auto run = [&](auto tag) -> int {
     using T = decltype(tag);

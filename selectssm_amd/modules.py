@@ -32,7 +32,7 @@ import torch
 import torch.nn.functional as F
 
 from .conv import conv1d_act
-from .scan import (_check_recursion, as_rows, bidirectional_selective_scan, resolve_chunking, scan_bwd,
+from .scan import (_check_recursion, as_rows, bidirectional_selective_scan, needs_grad, resolve_chunking, scan_bwd,
                    scan_bwd_pair, scan_fwd, scan_fwd_pair, selective_scan)
 
 _FUSED_CONV_ACTS = ("silu", "relu", None)
@@ -193,10 +193,12 @@ def _core_project(u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, N, rank):
     return A, dt_low, dt.contiguous(), Bc, Cc
 
 
-def _core_forward(u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, Dp, z, N, rank, reverse, complement, y_out=None):
-    """Projections + scan (selectssm.py:190-238); returns (y, saved tensors)."""
+def _core_forward(u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, Dp, z, N, rank, reverse, complement, want_ckpt, y_out=None):
+    """Projections + scan (selectssm.py:190-238); returns (y, saved tensors).  The scan
+    writes its checkpoints only when ``want_ckpt`` (a backward will run)."""
     A, dt_low, dt, Bc, Cc = _core_project(u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, N, rank)
-    y, ckpt = scan_fwd(u, dt, A, Bc, Cc, Dp, z, reverse, complement, delta_softplus=True, y_out=y_out)
+    y, ckpt = scan_fwd(u, dt, A, Bc, Cc, Dp, z, reverse, complement, want_ckpt=want_ckpt, delta_softplus=True,
+                       y_out=y_out)
     return y, (u, A, Wbc, Wdt, Wp, Dp, z, dt_low, dt, Bc, Cc, ckpt)
 
 
@@ -273,8 +275,8 @@ class _SSMCoreFn(torch.autograd.Function):
     beta = 1) instead of separate addition kernels."""
 
     @staticmethod
-    def forward(ctx, u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, Dp, z, N, rank, reverse, complement):
-        y, saved = _core_forward(u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, Dp, z, N, rank, reverse, complement)
+    def forward(ctx, u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, Dp, z, N, rank, reverse, complement, want_ckpt):
+        y, saved = _core_forward(u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, Dp, z, N, rank, reverse, complement, want_ckpt)
         ctx.save_for_backward(*saved)
         ctx.cfg = (N, rank, reverse, complement)
         return y
@@ -282,7 +284,7 @@ class _SSMCoreFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy):
         dy, _ = as_rows(dy, ctx.saved_tensors[0].dtype)
-        return (*_core_backward(ctx.saved_tensors, dy, *ctx.cfg), None, None, None, None)
+        return (*_core_backward(ctx.saved_tensors, dy, *ctx.cfg), None, None, None, None, None)
 
 
 class _PairCoreFn(torch.autograd.Function):
@@ -291,14 +293,14 @@ class _PairCoreFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, uf, A_logf, Wbcf, bbcf, Wdtf, bdtf, Wpf, bpf, Df, zf,
-                ur, A_logr, Wbcr, bbcr, Wdtr, bdtr, Wpr, bpr, Dr, zr, N, rank, complement):
+                ur, A_logr, Wbcr, bbcr, Wdtr, bdtr, Wpr, bpr, Dr, zr, N, rank, complement, want_ckpt):
         B_, L_, E = uf.shape
         y = torch.empty(B_, L_, 2 * E, dtype=uf.dtype, device=uf.device)
         pf = _core_project(uf, A_logf, Wbcf, bbcf, Wdtf, bdtf, Wpf, bpf, N, rank)
         pr = _core_project(ur, A_logr, Wbcr, bbcr, Wdtr, bdtr, Wpr, bpr, N, rank)
         # both directions' scans in one pair call (their time-split aggregate passes share a launch)
         calls = [dict(u=u, delta=p[2], A=p[0], B=p[3], C=p[4], Dskip=Dp, z=z, reverse=rev, complement=comp,
-                      delta_softplus=True, y_out=yo)
+                      delta_softplus=True, y_out=yo, want_ckpt=want_ckpt)
                  for u, p, Dp, z, rev, comp, yo in ((uf, pf, Df, zf, False, False, y[..., :E]),
                                                     (ur, pr, Dr, zr, True, complement, y[..., E:]))]
         (_, ckf), (_, ckr) = scan_fwd_pair(calls)
@@ -319,7 +321,7 @@ class _PairCoreFn(torch.autograd.Function):
                                           dict(_scan_call(sr, True, complement), ckpt=sr[-1], dy=dy[..., E:])])
         gf = _core_param_grads(sf, scan_gf, N, rank)
         gr = _core_param_grads(sr, scan_gr, N, rank)
-        return (*gf, *gr, None, None, None)
+        return (*gf, *gr, None, None, None, None)
 
 
 class SelectiveSSM(_FlaxModule):
@@ -418,7 +420,7 @@ class SelectiveSSM(_FlaxModule):
             u = _activation_fn(self.activation)(u)
         if not projections:
             if self.custom_vjp_scan or self.recursive_scan:
-                _check_recursion(self.min_recursion_length, self.recursive_split)
+                _check_recursion(L, self.min_recursion_length, self.recursive_split)
             else:
                 resolve_chunking(L, D, self.chunk_size, self.n_channel_groups)
             if not self.dt_proj_enabled and self.rank > 1 and D % self.rank != 0:
@@ -448,7 +450,7 @@ class SelectiveSSM(_FlaxModule):
 
         # the reference's strategy dispatch (selectssm.py:223-228) and its argument checks
         if self.custom_vjp_scan or self.recursive_scan:
-            _check_recursion(self.min_recursion_length, self.recursive_split)
+            _check_recursion(L, self.min_recursion_length, self.recursive_split)
         else:
             resolve_chunking(L, D, self.chunk_size, self.n_channel_groups)
         return dict(u=u, delta=dt, A=A, B=Bc, C=Cc, D=self.D)
@@ -507,8 +509,9 @@ class SelectiveSSM(_FlaxModule):
     def _core(self, u: torch.Tensor, z: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Projections + scan from the conv output u in one autograd node (see _SSMCoreFn)."""
         zz = None if z is None else as_rows(z, u.dtype)[0]
-        return _SSMCoreFn.apply(*self._core_args(u, zz), self.hidden_features, self.rank, self.reverse,
-                                self.complement)
+        args = self._core_args(u, zz)
+        return _SSMCoreFn.apply(*args, self.hidden_features, self.rank, self.reverse, self.complement,
+                                needs_grad(*args))
 
 
 class RMSNorm(torch.nn.Module):
@@ -680,8 +683,8 @@ class BidirectionalMamba(_FlaxModule):
                 uf = f._prepare(xf, projections=False)["u"]
                 ur = r._prepare(xr, projections=False)["u"]
                 io = uf.dtype
-                x = _PairCoreFn.apply(*f._core_args(uf, as_rows(zf, io)[0]), *r._core_args(ur, as_rows(zr, io)[0]),
-                                      f.hidden_features, f.rank, self.complement)
+                args = (*f._core_args(uf, as_rows(zf, io)[0]), *r._core_args(ur, as_rows(zr, io)[0]))
+                x = _PairCoreFn.apply(*args, f.hidden_features, f.rank, self.complement, needs_grad(*args))
             f._finish(None)
             r._finish(None)
         else:

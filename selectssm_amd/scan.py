@@ -137,6 +137,15 @@ def as_rows(t, dtype):
     return t, t.shape[-1]
 
 
+def needs_grad(*ts) -> bool:
+    """Whether an autograd graph will be recorded for an op on ``ts``: grad mode is
+    on and some input requires a gradient.  Decided before ``Function.apply``,
+    since inside ``forward`` grad mode is off and ``ctx.needs_input_grad`` does
+    not reflect an enclosing ``torch.no_grad()``.  Only then are the forward's
+    checkpoints (the backward's residuals) written."""
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
+
+
 def _scratch(nbytes, device):
     return torch.empty(nbytes // 4, dtype=torch.float32, device=device) if nbytes else None
 
@@ -260,9 +269,8 @@ class SelectiveScanFn(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, u, delta, A, B, C, Dskip, z, reverse, complement, segments=0, delta_softplus=False):
-        y, ckpt = scan_fwd(u, delta, A, B, C, Dskip, z, reverse, complement,
-                           want_ckpt=torch.is_grad_enabled() or any(ctx.needs_input_grad), segments=segments,
+    def forward(ctx, u, delta, A, B, C, Dskip, z, reverse, complement, segments, delta_softplus, want_ckpt):
+        y, ckpt = scan_fwd(u, delta, A, B, C, Dskip, z, reverse, complement, want_ckpt=want_ckpt, segments=segments,
                            delta_softplus=delta_softplus)
         ctx.save_for_backward(u, delta, A, B, C, Dskip, z, ckpt)
         ctx.flags = (reverse, complement)
@@ -276,7 +284,7 @@ class SelectiveScanFn(torch.autograd.Function):
         dy, _ = as_rows(dy, u.dtype)
         du, ddelta, dA, dB, dC, dD, dz = scan_bwd(u, delta, A, B, C, Dskip, z, ckpt, dy, *ctx.flags,
                                                   segments=ctx.segments, delta_softplus=ctx.delta_softplus)
-        return du, ddelta, dA, dB, dC, dD, dz, None, None, None, None
+        return du, ddelta, dA, dB, dC, dD, dz, None, None, None, None, None
 
 
 def selective_scan(u, delta, A, B, C, D=None, z=None, reverse=False, complement=False, segments=0,
@@ -306,7 +314,8 @@ def selective_scan(u, delta, A, B, C, D=None, z=None, reverse=False, complement=
     if not 0 <= int(segments) <= 1024:
         raise ValueError(f"segments must be in 0..1024, got {segments}")
     return SelectiveScanFn.apply(cast(u), cast(delta), fcast(A), cast(B), cast(C), fcast(D), as_rows(z, io)[0],
-                                 bool(reverse), bool(complement), int(segments), bool(delta_softplus))
+                                 bool(reverse), bool(complement), int(segments), bool(delta_softplus),
+                                 needs_grad(u, delta, A, B, C, D, z))
 
 
 class BidirectionalScanFn(torch.autograd.Function):
@@ -315,10 +324,9 @@ class BidirectionalScanFn(torch.autograd.Function):
     each with its D skip and silu(z) gate fused (selectssm.py:325-336)."""
 
     @staticmethod
-    def forward(ctx, uf, dtf, Af, Bf, Cf, Df, zf, ur, dtr, Ar, Br, Cr, Dr, zr, complement, delta_softplus):
+    def forward(ctx, uf, dtf, Af, Bf, Cf, Df, zf, ur, dtr, Ar, Br, Cr, Dr, zr, complement, delta_softplus, want):
         Bt, Ln, D = uf.shape
         y = torch.empty(Bt, Ln, 2 * D, dtype=uf.dtype, device=uf.device)
-        want = torch.is_grad_enabled() or any(ctx.needs_input_grad)
         # one pair call: the time-split aggregate passes of both directions share a launch
         (_, ckf), (_, ckr) = scan_fwd_pair([
             dict(u=uf, delta=dtf, A=Af, B=Bf, C=Cf, Dskip=Df, z=zf, want_ckpt=want, delta_softplus=delta_softplus,
@@ -339,7 +347,7 @@ class BidirectionalScanFn(torch.autograd.Function):
             dict(u=uf, delta=dtf, A=Af, B=Bf, C=Cf, Dskip=Df, z=zf, ckpt=ckf, dy=dy[..., :D], delta_softplus=dsp),
             dict(u=ur, delta=dtr, A=Ar, B=Br, C=Cr, Dskip=Dr, z=zr, ckpt=ckr, dy=dy[..., D:], reverse=True,
                  complement=complement, delta_softplus=dsp)])
-        return (*gf, *gr, None, None)
+        return (*gf, *gr, None, None, None)
 
 
 def bidirectional_selective_scan(fwd, rev, complement=False, delta_softplus=False):
@@ -360,7 +368,8 @@ def bidirectional_selective_scan(fwd, rev, complement=False, delta_softplus=Fals
                  as_rows(d.get("z"), io)[0]]
     if fwd["u"].shape != rev["u"].shape:
         raise ValueError("the two directions must have the same (B, L, D)")
-    return BidirectionalScanFn.apply(*args, bool(complement), bool(delta_softplus))
+    want = needs_grad(*(d.get(k) for d in (fwd, rev) for k in ("u", "delta", "A", "B", "C", "D", "z")))
+    return BidirectionalScanFn.apply(*args, bool(complement), bool(delta_softplus), want)
 
 
 # ------------------------------------------------------- reference-named API
@@ -377,15 +386,29 @@ def ssm_chunked_scan(x, Acoeff, Bcoeff, Ccoeff, dt, chunk_size: int = None, n_ch
     return selective_scan(x, dt, Acoeff, Bcoeff, Ccoeff)
 
 
-def _check_recursion(min_recursion_length, recursive_split):
-    if recursive_split < 2:
-        # the reference recurses without end for split 1 (ssmrecscan.py:56-63)
+def _check_recursion(L_, min_recursion_length, recursive_split):
+    """The reference's recursion test at the top level (ssmrecscan.py:56): it splits a
+    chunk only while ``len > min_recursion_length and len % recursive_split == 0``.
+    A row that short never recurses and returns a result whatever the split; a
+    split of 1 that does recurse never shortens the chunk (the reference recurses
+    without end), and a split of 0 divides by zero in that test."""
+    if L_ <= min_recursion_length:
+        return
+    if recursive_split == 0:
+        raise ZeroDivisionError("integer division or modulo by zero (recursive_split=0)")
+    if L_ % recursive_split != 0:
+        return
+    if recursive_split == 1:
         raise RecursionError(f"recursive_split={recursive_split} never shortens the sequence")
+    if recursive_split < 0:
+        raise ValueError(f"recursive_split={recursive_split} must be positive")
 
 
 def ssm_recursive_scan(x, Acoeff, Bcoeff, Ccoeff, Delta, min_recursion_length: int = 2, recursive_split: int = 2):
     """Drop-in for ``ssm_recursive_scan`` (ssmrecscan.py:36-77)."""
-    _check_recursion(min_recursion_length, recursive_split)
+    if x.dim() != 3:
+        raise ValueError(f"x must be (B, L, D), got shape {tuple(x.shape)}")
+    _check_recursion(x.shape[-2], min_recursion_length, recursive_split)
     return selective_scan(x, Delta, Acoeff, Bcoeff, Ccoeff)
 
 
@@ -395,5 +418,7 @@ def ssm_scan(x, Acoeff, Bcoeff, Ccoeff, Delta, min_recursion_length: int = 2, re
     Its gradient is the custom VJP's adjoint (du, dA, dB, dC, ddelta), computed
     by ``ssm_bwd`` from the inputs and the forward's checkpoints.
     """
-    _check_recursion(min_recursion_length, recursive_split)
+    if x.dim() != 3:
+        raise ValueError(f"x must be (B, L, D), got shape {tuple(x.shape)}")
+    _check_recursion(x.shape[-2], min_recursion_length, recursive_split)
     return selective_scan(x, Delta, Acoeff, Bcoeff, Ccoeff)

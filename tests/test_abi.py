@@ -155,3 +155,18 @@ def test_pair_entry_points_validate_before_launching():
     assert b"NULL" in lib.ssm_last_error()
     bio = (L.SsmBwdIo * 2)()
     assert lib.ssm_bwd_pair(None, descs, bio) == L.SSM_ERR_INVALID
+
+
+def test_pair_rejects_mixed_dtypes_before_launching():
+    """A pair runs one element type: an f32 desc with a bf16 desc is an invalid request
+    (its second call would otherwise run f32 kernels over bf16 buffers)."""
+    lib = L.lib()
+    p = ctypes.c_void_p(16)
+    for first, second in ((L.SSM_F32, L.SSM_BF16), (L.SSM_BF16, L.SSM_F32)):
+        descs = (L.SsmDesc * 2)(L.make_desc(2, 64, 64, 16, dtype=first), L.make_desc(2, 64, 64, 16, dtype=second))
+        fio = (L.SsmFwdIo * 2)(*[L.SsmFwdIo(p, p, p, p, p, None, None, p, None, None)] * 2)
+        assert lib.ssm_fwd_pair(None, descs, fio) == L.SSM_ERR_INVALID
+        assert b"same dtype" in lib.ssm_last_error()
+        bio = (L.SsmBwdIo * 2)(*[L.SsmBwdIo(p, p, p, p, p, None, None, p, p, p, p, p, p, p, None, None, p)] * 2)
+        assert lib.ssm_bwd_pair(None, descs, bio) == L.SSM_ERR_INVALID
+        assert b"same dtype" in lib.ssm_last_error()

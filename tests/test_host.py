@@ -62,6 +62,22 @@ def test_reference_errors_raised_before_any_gpu_work():
         selectssm_amd.ssm_recursive_scan(u, A, B, C, dt, recursive_split=1)
 
 
+def test_recursion_check_follows_the_reference_condition():
+    """ssmrecscan.py:56 recurses only while len > min_recursion_length and
+    len % recursive_split == 0: a short row never recurses (any split returns a
+    result), split 1 recursing never ends, split 0 divides by zero in the test."""
+    from selectssm_amd.scan import _check_recursion
+
+    for L_, ml, sp in ((2, 2, 1), (1, 2, 0), (5, 8, 1), (97, 2, 2), (96, 2, 2), (81, 2, 3), (7, 2, 2)):
+        _check_recursion(L_, ml, sp)  # no error
+    with pytest.raises(RecursionError):
+        _check_recursion(3, 2, 1)
+    with pytest.raises(ZeroDivisionError):
+        _check_recursion(3, 2, 0)
+    with pytest.raises(ValueError):
+        _check_recursion(8, 2, -2)
+
+
 def test_missing_library_fails_loudly(tmp_path, monkeypatch):
     from selectssm_amd import _lib
 

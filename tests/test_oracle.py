@@ -10,6 +10,7 @@ other.  Each check is chosen so a plausible slip (a dropped term, an
 off-by-one in the decay product, a wrong sign, transposed operands) fails it.
 """
 import math
+import zlib
 
 import numpy as np
 import pytest
@@ -421,3 +422,160 @@ def test_selective_ssm_reduces_to_scan_plus_skip():
     dt = O.softplus(x @ p["dt"]["kernel"] + p["dt"]["bias"])
     ref = O.scan_forward(x, dt, -np.exp(p["A_log"]), BC[..., :4], BC[..., 4:]) + x * p["D"]
     np.testing.assert_allclose(y, ref, rtol=1e-12)
+
+
+# ----------------------------------------------------- module-level functions
+
+def test_norms_closed_forms_and_torch():
+    """rms_norm / layer_norm (Flax RMSNorm / LayerNorm, epsilon 1e-6) on rows whose
+    result is known in closed form, and against torch's fp64 library routines."""
+    import torch
+    import torch.nn.functional as F
+
+    eps = 1e-6
+    scale = np.array([0.5, 1.0, 2.0, -1.5, 3.0, 0.25])
+    bias = np.array([0.1, -0.2, 0.3, 0.0, 1.0, -1.0])
+    c = 3.0
+    const = np.full((1, 1, 6), c)
+    alt = np.array([[[c, -c, c, -c, c, -c]]])
+    # constant row: rms = |c|; mean = c, variance 0
+    np.testing.assert_allclose(O.rms_norm(const, scale), (c / math.sqrt(c * c + eps)) * scale[None, None], rtol=1e-14)
+    np.testing.assert_allclose(O.layer_norm(const, scale, bias), np.broadcast_to(bias, (1, 1, 6)), atol=1e-14)
+    # sign-alternating row: rms = |c|; mean 0, variance c^2
+    sgn = np.array([1, -1, 1, -1, 1, -1], dtype=np.float64)
+    np.testing.assert_allclose(O.rms_norm(alt, scale)[0, 0], (c / math.sqrt(c * c + eps)) * sgn * scale, rtol=1e-14)
+    np.testing.assert_allclose(O.layer_norm(alt, scale, bias)[0, 0], (c / math.sqrt(c * c + eps)) * sgn * scale + bias,
+                               rtol=1e-14)
+    # a row with mean != 0: layer_norm centres, rms_norm does not
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal((2, 5, 6)) + 2.0
+    xt = torch.from_numpy(x)
+    ref_rms = F.rms_norm(xt, (6,), torch.from_numpy(scale), eps).numpy()
+    ref_ln = F.layer_norm(xt, (6,), torch.from_numpy(scale), torch.from_numpy(bias), eps).numpy()
+    np.testing.assert_allclose(O.rms_norm(x, scale), ref_rms, rtol=1e-12)
+    np.testing.assert_allclose(O.layer_norm(x, scale, bias), ref_ln, rtol=1e-12, atol=1e-14)
+    assert not np.allclose(O.rms_norm(x, scale), ref_ln)
+
+
+def test_gelu_tanh_identities_and_torch():
+    """gelu_tanh: gelu(0) = 0, gelu(x) - gelu(-x) = x (the tanh term is odd),
+    gelu(x) -> x for large x and -> 0 for large -x, and torch's tanh-approximate gelu in fp64."""
+    import torch
+    import torch.nn.functional as F
+
+    x = np.linspace(-6.0, 6.0, 241)
+    g = O.gelu_tanh(x)
+    assert O.gelu_tanh(np.array([0.0]))[0] == 0.0
+    np.testing.assert_allclose(g - O.gelu_tanh(-x), x, rtol=1e-13, atol=1e-14)
+    np.testing.assert_allclose(O.gelu_tanh(np.array([30.0, -30.0])), [30.0, 0.0], atol=1e-12)
+    np.testing.assert_allclose(g, F.gelu(torch.from_numpy(x), approximate="tanh").numpy(), rtol=1e-13, atol=1e-15)
+    # and it is not the erf form (flax.linen.gelu's default is approximate=True)
+    assert not np.allclose(g, F.gelu(torch.from_numpy(x)).numpy(), rtol=1e-6, atol=1e-9)
+    np.testing.assert_allclose(O.activate(x, "gelu"), g, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("R", [2, 6])
+def test_selective_ssm_dt_proj_branch_is_composed_dense(R):
+    """dt = softplus(dt_proj(dt(u))) (selectssm.py:195-210) with a non-square
+    (R < D) and a square non-symmetric dt_proj: equal to one Dense whose kernel
+    is dt.kernel @ dt_proj.kernel (and bias dt.bias @ dt_proj.kernel + dt_proj.bias),
+    run through the dt_proj=False path with dt_rank = D (no repeat)."""
+    rng = np.random.default_rng(31 + R)
+    D = 6
+    x = rng.standard_normal((2, 14, D))
+    p = _ssm_params(rng, D, R=R)
+    Wd, bd = p["dt"]["kernel"], p["dt"]["bias"]
+    Wp, bp = p["dt_proj"]["kernel"], p["dt_proj"]["bias"]
+    merged = {k: v for k, v in p.items() if k not in ("dt", "dt_proj")}
+    merged["dt"] = {"kernel": Wd @ Wp, "bias": bd @ Wp + bp}
+    y = O.selective_ssm_forward(p, x, hidden_features=4, dt_rank=R, dt_proj=True)
+    ref = O.selective_ssm_forward(merged, x, hidden_features=4, dt_rank=D, dt_proj=False)
+    np.testing.assert_allclose(y, ref, rtol=1e-11, atol=1e-12)
+    if R == D:
+        # a transposed dt_proj kernel would give another answer
+        swapped = dict(p, dt_proj={"kernel": Wp.T.copy(), "bias": bp})
+        assert not np.allclose(O.selective_ssm_forward(swapped, x, hidden_features=4, dt_rank=R), y)
+
+
+def _bm_case(rng, Dm, E, N, tie_in, tie_gate, concat, norm, mlp, dt_proj):
+    """Parameters of a BidirectionalMamba built from separately drawn sub-kernels
+    (in_proj's column blocks xf, xr, zf, zr in the reference's order,
+    selectssm.py:319), plus the expected output assembled from those blocks
+    directly: norm -> each block's own Dense -> SelectiveSSM pair -> gate ->
+    concat or sum -> out_proj -> residual (selectssm.py:306-362)."""
+    ED = math.ceil(E * Dm)
+    R = -(-Dm // 16)  # dt_rank 'auto' from the block's input width (selectssm.py:286-289)
+    blk = {k: {"kernel": rng.standard_normal((Dm, ED)) / np.sqrt(Dm), "bias": rng.standard_normal(ED) * 0.1}
+           for k in ("xf", "xr", "zf", "zr")}
+    order = ["xf"] + ([] if tie_in else ["xr"]) + ["zf"] + ([] if tie_gate else ["zr"])
+    p = {"in_proj": {"kernel": np.concatenate([blk[k]["kernel"] for k in order], axis=1),
+                     "bias": np.concatenate([blk[k]["bias"] for k in order])},
+         "ssm_fwd": _ssm_params(rng, ED, N=N, K=4, R=R, dt_proj=dt_proj),
+         "ssm_rev": _ssm_params(rng, ED, N=N, K=4, R=R, dt_proj=dt_proj),
+         "out_proj": {"kernel": rng.standard_normal((2 * ED if concat else ED, Dm)) / np.sqrt(ED),
+                      "bias": rng.standard_normal(Dm) * 0.1}}
+    if norm == "rms":
+        p["RMSNorm_0"] = {"scale": rng.uniform(0.5, 1.5, Dm)}
+    else:
+        p["LayerNorm_0"] = {"scale": rng.uniform(0.5, 1.5, Dm), "bias": rng.standard_normal(Dm) * 0.1}
+    if mlp:
+        p["mlp"] = {"kernel": rng.standard_normal((Dm, 2 * Dm)) / np.sqrt(Dm), "bias": rng.standard_normal(2 * Dm) * .1}
+        p["mlp_proj"] = {"kernel": rng.standard_normal((2 * Dm, Dm)) / np.sqrt(2 * Dm),
+                         "bias": rng.standard_normal(Dm) * 0.1}
+    return p, blk, ED, R
+
+
+@pytest.mark.parametrize("tie_in,tie_gate", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("concat,complement,norm,mlp,dt_proj", [
+    (True, True, "rms", False, True), (False, False, "layer", True, True), (True, False, "rms", False, False)])
+def test_bidirectional_mamba_is_composition_of_blocks(tie_in, tie_gate, concat, complement, norm, mlp, dt_proj):
+    rng = np.random.default_rng(zlib.crc32(repr((tie_in, tie_gate, concat, complement, norm, mlp, dt_proj)).encode()))
+    Dm, E, N = 32, 1.5, 4
+    p, blk, ED, R = _bm_case(rng, Dm, E, N, tie_in, tie_gate, concat, norm, mlp, dt_proj)
+    x = rng.standard_normal((2, 12, Dm))
+    got = O.bidirectional_mamba_forward(p, x, N, E, complement=complement, tie_in_proj=tie_in, tie_gate=tie_gate,
+                                        concatenate_fwd_rev=concat, norm_type=norm, mlp_layer=mlp,
+                                        ssm_args={"dt_proj": dt_proj})
+    # expected, assembled from the named blocks (no split offsets)
+    if norm == "rms":
+        xn = x / np.sqrt(np.mean(x * x, -1, keepdims=True) + 1e-6) * p["RMSNorm_0"]["scale"]
+    else:
+        m = x.mean(-1, keepdims=True)
+        xn = (x - m) / np.sqrt(((x - m) ** 2).mean(-1, keepdims=True) + 1e-6) * p["LayerNorm_0"]["scale"] \
+            + p["LayerNorm_0"]["bias"]
+    proj = {k: xn @ v["kernel"] + v["bias"] for k, v in blk.items()}
+    xf, zf = proj["xf"], proj["zf"]
+    xr = xf if tie_in else proj["xr"]
+    zr = zf if tie_gate else proj["zr"]
+    yf = O.selective_ssm_forward(p["ssm_fwd"], xf, hidden_features=N, dt_rank=R, dt_proj=dt_proj) * O.silu(zf)
+    yr = O.selective_ssm_forward(p["ssm_rev"], xr, reverse=True, complement=complement, hidden_features=N,
+                                 dt_rank=R, dt_proj=dt_proj) * O.silu(zr)
+    mix = np.concatenate([yf, yr], -1) if concat else yf + yr
+    ref = x + mix @ p["out_proj"]["kernel"] + p["out_proj"]["bias"]
+    if mlp:
+        h1 = ref @ p["mlp"]["kernel"] + p["mlp"]["bias"]
+        ref = ref + O.silu(h1) @ p["mlp_proj"]["kernel"] + p["mlp_proj"]["bias"]
+    np.testing.assert_allclose(got, ref, rtol=1e-11, atol=1e-12)
+    # the check sees the wiring: the directions' inputs or gates exchanged give another answer
+    if not tie_in or not tie_gate:
+        yf2 = O.selective_ssm_forward(p["ssm_fwd"], xr, hidden_features=N, dt_rank=R, dt_proj=dt_proj) * O.silu(zr)
+        yr2 = O.selective_ssm_forward(p["ssm_rev"], xf, reverse=True, complement=complement, hidden_features=N,
+                                      dt_rank=R, dt_proj=dt_proj) * O.silu(zf)
+        mix2 = np.concatenate([yf2, yr2], -1) if concat else yf2 + yr2
+        assert not np.allclose(x + mix2 @ p["out_proj"]["kernel"] + p["out_proj"]["bias"], ref)
+
+
+def test_bidirectional_mamba_dt_rank_comes_from_block_width():
+    """dt_rank='auto' is ceil(d_model / 16) of the block's input, not of the SSM width
+    E*d_model (selectssm.py:286-289, 325-326): with dt_proj=False the low-rank dt is
+    repeated D_inner / dt_rank times, so the other choice cannot even be evaluated."""
+    rng = np.random.default_rng(40)
+    Dm, E, N = 32, 2.0, 4
+    p, _, ED, R = _bm_case(rng, Dm, E, N, True, True, True, "rms", False, False)
+    assert (R, ED) == (2, 64)
+    x = rng.standard_normal((1, 8, Dm))
+    y = O.bidirectional_mamba_forward(p, x, N, E, tie_in_proj=True, tie_gate=True, ssm_args={"dt_proj": False})
+    assert np.isfinite(y).all()
+    with pytest.raises(ValueError):
+        O.bidirectional_mamba_forward(p, x, N, E, dt_rank=math.ceil(ED / 16), tie_in_proj=True, tie_gate=True,
+                                      ssm_args={"dt_proj": False})
