@@ -15,7 +15,11 @@ pytestmark = pytest.mark.gpu
 
 
 def _peak(fn):
-    """(result, high-water allocation above what was live before fn)."""
+    """(result, high-water allocation above what was live before fn).  fn runs once
+    before the measured call, so one-time allocations (e.g. a GEMM library's
+    workspace on its first use) are not counted."""
+    with torch.no_grad():
+        fn()
     torch.cuda.synchronize()
     base = torch.cuda.memory_allocated()
     torch.cuda.reset_peak_memory_stats()
