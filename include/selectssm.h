@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define SSM_ABI_VERSION 4
+#define SSM_ABI_VERSION 5
 
 /* error codes */
 #define SSM_OK 0
@@ -123,6 +123,28 @@ int ssm_bwd(void* stream, const ssm_desc_t* desc,
             const float* ckpt, const void* dy,
             void* du, void* ddelta, float* dA, void* dB, void* dC,
             float* dD, void* dz, void* workspace);
+
+/* Size of the static device scratch that ssm_bwd_static uses in place of a workspace. */
+#define SSM_STATIC_SCRATCH_BYTES (64u << 20)
+
+/*
+ * ssm_bwd without a workspace argument, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference: it exists for those callers.
+ * The workspace is a static device array of SSM_STATIC_SCRATCH_BYTES (64 MiB)
+ * that each GPU holds until the process ends; a desc whose
+ * ssm_bwd_workspace_bytes exceeds it is rejected with SSM_ERR_INVALID (call
+ * ssm_bwd then).  Same results as ssm_bwd, bit for bit.  The stream must
+ * belong to the current device.  Calls that overlap on one GPU share the
+ * scratch and race: serialise them (one stream, or events).  Allocates
+ * nothing (no hipMalloc / hipFree, no allocating library routine).
+ */
+int ssm_bwd_static(void* stream, const ssm_desc_t* desc,
+                   const void* u, const void* delta, const float* A,
+                   const void* Bc, const void* Cc, const float* Dskip, const void* z,
+                   const float* ckpt, const void* dy,
+                   void* du, void* ddelta, float* dA, void* dB, void* dC,
+                   float* dD, void* dz);
 
 /* Buffers of one ssm_fwd call (same meaning and requirements). */
 typedef struct {

@@ -28,7 +28,9 @@ SSM_ACT_NONE = 0
 SSM_ACT_SILU = 1
 SSM_ACT_RELU = 2
 
-ABI_VERSION = 4
+ABI_VERSION = 5
+
+STATIC_SCRATCH_BYTES = 64 << 20  # SSM_STATIC_SCRATCH_BYTES: ssm_bwd_static's workspace
 
 # every symbol include/selectssm.h declares
 EXPORTS = (
@@ -39,6 +41,7 @@ EXPORTS = (
     "ssm_bwd_workspace_bytes",
     "ssm_fwd",
     "ssm_bwd",
+    "ssm_bwd_static",
     "ssm_fwd_pair",
     "ssm_bwd_pair",
     "ssm_conv_bwd_workspace_bytes",
@@ -124,6 +127,8 @@ def _declare(lib):
     lib.ssm_fwd.argtypes = [vp, dp, vp, vp, fp, vp, vp, fp, vp, vp, fp, vp]
     lib.ssm_bwd.restype = ctypes.c_int
     lib.ssm_bwd.argtypes = [vp, dp, vp, vp, fp, vp, vp, fp, vp, fp, vp, vp, vp, fp, vp, vp, fp, vp, vp]
+    lib.ssm_bwd_static.restype = ctypes.c_int
+    lib.ssm_bwd_static.argtypes = [vp, dp, vp, vp, fp, vp, vp, fp, vp, fp, vp, vp, vp, fp, vp, vp, fp, vp]
     lib.ssm_fwd_pair.restype = ctypes.c_int
     lib.ssm_fwd_pair.argtypes = [vp, dp, ctypes.POINTER(SsmFwdIo)]
     lib.ssm_bwd_pair.restype = ctypes.c_int

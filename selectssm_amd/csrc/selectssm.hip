@@ -50,6 +50,7 @@
 #include <cstdint>
 #include <algorithm>
 #include <cstdio>
+#include <mutex>
 #include <string>
 #include <type_traits>
 
@@ -1657,6 +1658,41 @@ int hip_check(hipError_t e, const char* what) {
 
 }  // namespace ssm
 
+// ------------------------------------------- static scratch (ssm_bwd_static)
+//
+// The workspace of ssm_bwd_static: a file-scope device array of fixed size.
+// Every GPU the library runs on holds its own copy until the process ends.  In
+// host code `scratch` only names the symbol; its device address on the
+// current device comes from hipGetSymbolAddress, looked up once per device and
+// kept.  Calls on one GPU share the array (overlapping calls race); no kernel
+// needs it cleared, since every partial the reductions read is written first
+// by the same call.
+static __device__ __align__(256) float scratch[SSM_STATIC_SCRATCH_BYTES / sizeof(float)];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The address of `scratch` on the current device (looked up on the first call there).
+int scratch_on_current_device(void** out) {
+  int dev = -1;
+  if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
+  if (dev < 0 || dev >= kMaxDevices) return fail(SSM_ERR_UNSUPPORTED, "device ordinal beyond 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    if (int rc = hip_check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)")) return rc;
+    if (ptr == nullptr) return fail(SSM_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return SSM_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 int ssm_abi_version(void) { return SSM_ABI_VERSION; }
@@ -1720,6 +1756,30 @@ int ssm_bwd(void* stream, const ssm_desc_t* desc, const void* u, const void* del
   return launch_bwd<bf16>(st, desc, s,
                           bwd_args<bf16>(desc, s, u, delta, A, Bc, Cc, Dskip, z, ckpt, dy, du, ddelta, dz, workspace),
                           dA, dB, dC, dD, ddelta, workspace, true);
+}
+
+int ssm_bwd_static(void* stream, const ssm_desc_t* desc, const void* u, const void* delta, const float* A,
+                   const void* Bc, const void* Cc, const float* Dskip, const void* z, const float* ckpt,
+                   const void* dy, void* du, void* ddelta, float* dA, void* dB, void* dC, float* dD, void* dz) {
+  g_last_error.clear();
+  Shape s;
+  if (int rc = validate(desc, &s)) return rc;
+  const size_t need = ws_layout(s, desc->delta_broadcast != 0).total * sizeof(float);
+  if (need > SSM_STATIC_SCRATCH_BYTES)
+    return fail(SSM_ERR_INVALID, "ssm_bwd_static: this desc needs " + std::to_string(need) +
+                                     " bytes of workspace, more than the static scratch's " +
+                                     std::to_string((size_t)SSM_STATIC_SCRATCH_BYTES) + " (use ssm_bwd)");
+  // the stream must belong to the current device, whose copy of the scratch is used
+  if (stream != nullptr) {
+    int sdev = -1, dev = -1;
+    if (int rc = hip_check(hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev), "hipStreamGetDevice"))
+      return rc;
+    if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
+    if (sdev != dev) return fail(SSM_ERR_INVALID, "ssm_bwd_static: the stream belongs to another device than the current one");
+  }
+  void* ws = nullptr;
+  if (int rc = scratch_on_current_device(&ws)) return rc;
+  return ssm_bwd(stream, desc, u, delta, A, Bc, Cc, Dskip, z, ckpt, dy, du, ddelta, dA, dB, dC, dD, dz, ws);
 }
 
 // The two calls of a pair as ssm_fwd / ssm_bwd would make them, with the

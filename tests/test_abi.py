@@ -36,6 +36,8 @@ def test_header_constants_match_binding():
               "SSM_ACT_NONE", "SSM_ACT_SILU", "SSM_ACT_RELU"):
         assert int(consts[k]) == getattr(L, k), k
     assert int(consts["SSM_ABI_VERSION"]) == L.ABI_VERSION
+    m = re.search(r"#define SSM_STATIC_SCRATCH_BYTES \((\d+)u << (\d+)\)", text)
+    assert m and int(m[1]) << int(m[2]) == L.STATIC_SCRATCH_BYTES
     assert ctypes.sizeof(L.SsmDesc) == 64
 
 
@@ -170,3 +172,17 @@ def test_pair_rejects_mixed_dtypes_before_launching():
         bio = (L.SsmBwdIo * 2)(*[L.SsmBwdIo(p, p, p, p, p, None, None, p, p, p, p, p, p, p, None, None, p)] * 2)
         assert lib.ssm_bwd_pair(None, descs, bio) == L.SSM_ERR_INVALID
         assert b"same dtype" in lib.ssm_last_error()
+
+
+def test_static_scratch_backward_rejects_oversized_workspace():
+    """ssm_bwd_static uses a fixed static scratch: a desc whose workspace exceeds it
+    is an invalid request, refused before any GPU work (config 1 needs 268 MB of
+    dB / dC partial sums)."""
+    lib = L.lib()
+    desc = L.make_desc(8, 8192, 2048, 16)
+    assert L.size_query(lib.ssm_bwd_workspace_bytes, desc) > L.STATIC_SCRATCH_BYTES
+    p = ctypes.c_void_p(16)
+    rc = lib.ssm_bwd_static(None, ctypes.byref(desc), *([p] * 5), None, None, p, p, p, p, p, p, p, None, None)
+    assert rc == L.SSM_ERR_INVALID
+    assert b"static scratch" in lib.ssm_last_error()
+    assert lib.ssm_bwd_static(None, None, *([p] * 16)) == L.SSM_ERR_INVALID
