@@ -11,7 +11,7 @@
  *     (a hipStream_t passed as void*; NULL means the legacy default stream).
  *   - Tensor layouts are the reference's: u, delta, y, z, dy, du, ddelta: (B,L,D)
  *     row-major (y, dy and z may have a longer row, desc.ld_y / ld_z);
- *     A, dA: (D,N); Bc, Cc, dB, dC: (B,L,N); Dskip, dD: (D,).
+ *     A, dA: (D,N); Bc, Cc, dB, dC: (B,L,N) (rows may be longer, desc.ld_bc); Dskip, dD: (D,).
  *     delta may be (B,L,1) (desc.delta_broadcast=1, selectssm.py:36, 203-210).
  *   - I/O element type is desc.dtype (f32 or bf16).  A, Dskip, dA, dD and the
  *     checkpoints are always f32; the recurrent state and every accumulator
@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define SSM_ABI_VERSION 5
+#define SSM_ABI_VERSION 6
 
 /* error codes */
 #define SSM_OK 0
@@ -69,6 +69,11 @@ typedef struct ssm_desc {
                              concatenated output (selectssm.py:335-336) */
   int64_t ld_z;           /* the same for z, e.g. z read in place from in_proj's output
                              (selectssm.py:319-321); 0 = dim.  dz is always (B,L,D) */
+  int64_t ld_bc;          /* elements between consecutive time rows of Bc, Cc, dB and dC; 0 = dstate.
+                             With ld_bc >= 2*dstate, Bc and Cc are column slices of one
+                             (B, L, ld_bc) array (batch stride L*ld_bc), e.g. read in place from
+                             SelectiveSSM's BC projection output (selectssm.py:191-192), and dB,
+                             dC are written into the matching slices of one gradient array */
 } ssm_desc_t;
 
 /* Version of this ABI (SSM_ABI_VERSION). */
@@ -164,10 +169,13 @@ typedef struct {
  * (resp. ssm_bwd) called for each in turn.  Replaces the forward and reverse
  * SSM calls of BidirectionalMamba (selectssm.py:325-326): when both descs
  * have the same shape (batch, seqlen, dim, dstate, dtype, delta_broadcast,
- * segments and SSM_DELTA_SOFTPLUS) and their rows are split in time, the
- * time-split aggregate passes of both run in one launch.  Each call keeps its
- * own time segments, so the results are bitwise those of the two calls.  The
- * two calls must not share an output or workspace buffer.
+ * segments and SSM_DELTA_SOFTPLUS), the two scans run as one launch of each
+ * kernel: the time-split aggregate passes always, the main passes when the
+ * two also need the same kernel variant (both with or both without the
+ * epilogue staging of SSM_GATE / reverse SSM_SKIP; forward: u and delta both
+ * 16-byte aligned or both not).  Each call keeps its own time segments, so the
+ * results are bitwise those of the two calls.  The two calls must not share
+ * an output or workspace buffer, and must have the same dtype.
  */
 int ssm_fwd_pair(void* stream, const ssm_desc_t* desc, const ssm_fwd_io_t* io);
 int ssm_bwd_pair(void* stream, const ssm_desc_t* desc, const ssm_bwd_io_t* io);

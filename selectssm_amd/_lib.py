@@ -28,7 +28,7 @@ SSM_ACT_NONE = 0
 SSM_ACT_SILU = 1
 SSM_ACT_RELU = 2
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 STATIC_SCRATCH_BYTES = 64 << 20  # SSM_STATIC_SCRATCH_BYTES: ssm_bwd_static's workspace
 
@@ -64,6 +64,7 @@ class SsmDesc(ctypes.Structure):
         ("segments", ctypes.c_int32),
         ("ld_y", ctypes.c_int64),
         ("ld_z", ctypes.c_int64),
+        ("ld_bc", ctypes.c_int64),
     ]
 
 
@@ -165,9 +166,9 @@ def check(code: int) -> None:
 
 
 def make_desc(batch, seqlen, dim, dstate, dtype=SSM_F32, flags=0, delta_broadcast=False, segments=0,
-              ld_y=0, ld_z=0) -> SsmDesc:
+              ld_y=0, ld_z=0, ld_bc=0) -> SsmDesc:
     return SsmDesc(int(batch), int(seqlen), int(dim), int(dstate), int(dtype), int(flags),
-                   1 if delta_broadcast else 0, int(segments), int(ld_y), int(ld_z))
+                   1 if delta_broadcast else 0, int(segments), int(ld_y), int(ld_z), int(ld_bc))
 
 
 def size_query(fn, desc, allow_zero=False) -> int:

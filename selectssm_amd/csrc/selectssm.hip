@@ -139,10 +139,25 @@ struct FwdArgs {
   float* agg_P;  // [B][nseg][N][D]: product of the segment's decays a_t
   int L, D, N, nblk;
   int ldy, ldz;       // row strides (elements) of y and z
+  int ldbc;           // row stride (elements) of B and C
   int seg_len, nseg;  // time segments per row (seg_len a multiple of kTT)
   int dstride;        // 1, or 0 for a (B,L,1) delta
   uint32_t flags;
 };
+
+// The arguments of the call a workgroup belongs to, picked field by field from
+// the two calls of a launch (a select of the structs' addresses would copy
+// both to scratch memory; per-field selects of uniform values stay in SGPRs).
+#define SSM_FWD_FIELDS(X)                                                                                     \
+  X(u) X(delta) X(A) X(Bc) X(Cc) X(Dskip) X(z) X(y) X(ckpt) X(agg_H) X(agg_P) X(L) X(D) X(N) X(nblk) X(ldy) \
+  X(ldz) X(ldbc) X(seg_len) X(nseg) X(dstride) X(flags)
+template <typename T>
+__device__ __forceinline__ FwdArgs<T> pick_args(const FwdArgs<T>& a0, const FwdArgs<T>& a1, bool second) {
+  FwdArgs<T> r;
+#define SSM_PICK(f) r.f = second ? a1.f : a0.f;
+  SSM_FWD_FIELDS(SSM_PICK)
+  return r;
+}
 
 // Staging of a forward tile (kTT steps x 64 channels) by the 256 threads:
 // thread -> column scol (channel cb*64 + scol), rows srow0 + k*4, k < 8.  A
@@ -161,8 +176,13 @@ struct FwdStage {
 // skip and the gate.  SP: delta arrives before softplus (SSM_DELTA_SOFTPLUS).
 // VEC: u and delta rows are read as aligned 4-element vectors (D % 4 == 0,
 // per-channel delta); chosen per launch, so every tile stages the same way.
+// Workgroups with blockIdx.y < rows0 scan rows of p0, the others rows of p1
+// (blockIdx.y - rows0): both directions of a BidirectionalMamba pass in one
+// launch.  A single call passes its arguments twice.
 template <int SPL, bool EPI, bool SP, bool VEC, typename T>
-__global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T> p) {
+__global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T> p0, FwdArgs<T> p1, int rows0) {
+  const bool second = (int)blockIdx.y >= rows0;
+  const FwdArgs<T> p = pick_args<T>(p0, p1, second);
   constexpr int NS = 4 * SPL;  // padded state count
   constexpr int NT = FwdStage::NT, RPT = FwdStage::RPT, RSTEP = FwdStage::RSTEP;
   constexpr int BCN = kTT * NS;                 // staged B (or C) elements per tile
@@ -175,7 +195,7 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 15;
   const int g = lane >> 4;
-  const int b = blockIdx.y;
+  const int b = second ? (int)blockIdx.y - rows0 : (int)blockIdx.y;
   const int cb = blockIdx.x;
   const int seg = blockIdx.z;
   const int L = p.L, D = p.D, N = p.N;
@@ -237,11 +257,11 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
   const T* __restrict__ dt_b = p.delta + (int64_t)b * L * dtD;
   const int ldy = p.ldy, ldz = p.ldz;
   const T* __restrict__ z_b = EPI ? p.z + (int64_t)b * L * ldz : nullptr;
-  const T* __restrict__ B_b = p.Bc + (int64_t)b * L * N;
-  const T* __restrict__ C_b = p.Cc + (int64_t)b * L * N;
+  const int ldbc = p.ldbc;
+  const T* __restrict__ B_b = p.Bc + (int64_t)b * L * ldbc;
+  const T* __restrict__ C_b = p.Cc + (int64_t)b * L * ldbc;
   T* __restrict__ y_b = p.y + (int64_t)b * L * ldy;
   float* __restrict__ ck_b = p.ckpt != nullptr ? p.ckpt + (int64_t)b * p.nblk * N * D : nullptr;
-  const int LN = L * N;
   const int ND = N * D;
   const buf_t ru = make_buf(u_b), rdt = make_buf(dt_b), rB = make_buf(B_b), rC = make_buf(C_b);
   const buf_t rz = make_buf(EPI ? z_b : u_b), ry = make_buf(y_b), rck = make_buf(ck_b != nullptr ? ck_b : p.A);
@@ -282,7 +302,7 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
       const int e = tid + k * NT;
       if (BCN % NT == 0 || e < BCN) {
         const int i = e / NS, n = e - (e / NS) * NS;
-        const uint32_t o = (uint32_t)(min((t0 + i) * N + min(n, N - 1), LN - 1) * sizeof(T));
+        const uint32_t o = (uint32_t)((min(t0 + i, L - 1) * ldbc + min(n, N - 1)) * sizeof(T));
         r_B[k] = bldr<T>(rB, o, 0);
         r_C[k] = bldr<T>(rC, o, 0);
       }
@@ -522,8 +542,8 @@ __device__ __forceinline__ void fwd_agg_body(const FwdArgs<T>& p, const int b) {
   const int scol_dt = p.dstride ? sdc : 0;
   const T* __restrict__ u_b = p.u + (int64_t)b * L * D;
   const T* __restrict__ dt_b = p.delta + (int64_t)b * L * dtD;
-  const T* __restrict__ B_b = p.Bc + (int64_t)b * L * N;
-  const int LN = L * N;
+  const int ldbc = p.ldbc;
+  const T* __restrict__ B_b = p.Bc + (int64_t)b * L * ldbc;
   const buf_t ru = make_buf(u_b), rdt = make_buf(dt_b), rB = make_buf(B_b);
   const uint32_t so_c = (uint32_t)(sdc * sizeof(T)), so_dt = (uint32_t)(scol_dt * sizeof(T));
   const uint32_t rowb = (uint32_t)(D * sizeof(T)), dtrowb = (uint32_t)(dtD * sizeof(T));
@@ -541,7 +561,7 @@ __device__ __forceinline__ void fwd_agg_body(const FwdArgs<T>& p, const int b) {
       const int e = tid + k * NT;
       if (BCN % NT == 0 || e < BCN) {
         const int i = e / NS, n = e - (e / NS) * NS;
-        r_B[k] = bldr<T>(rB, (uint32_t)(min((t0 + i) * N + min(n, N - 1), LN - 1) * sizeof(T)), 0);
+        r_B[k] = bldr<T>(rB, (uint32_t)((min(t0 + i, L - 1) * ldbc + min(n, N - 1)) * sizeof(T)), 0);
       }
     }
   };
@@ -652,10 +672,23 @@ struct BwdArgs {
   float* agg_P;   // [B][nseg][N][D]: product of the segment's decays a_t
   int Bt, L, D, N, nblk, ncb;
   int ldy, ldz;   // row strides (elements) of dy and of z
+  int ldbc;       // row stride (elements) of B and C
   int seg_len, nseg;
   int dstride;
   uint32_t flags;
 };
+
+#define SSM_BWD_FIELDS(X)                                                                                     \
+  X(u) X(delta) X(A) X(Bc) X(Cc) X(Dskip) X(z) X(ckpt) X(dy) X(du) X(ddelta) X(dz) X(ws_dB) X(ws_dC) X(ws_dA) \
+  X(ws_dD) X(ws_ddt) X(agg_G) X(agg_P) X(Bt) X(L) X(D) X(N) X(nblk) X(ncb) X(ldy) X(ldz) X(ldbc) X(seg_len)   \
+  X(nseg) X(dstride) X(flags)
+template <typename T>
+__device__ __forceinline__ BwdArgs<T> pick_args(const BwdArgs<T>& a0, const BwdArgs<T>& a1, bool second) {
+  BwdArgs<T> r;
+  SSM_BWD_FIELDS(SSM_PICK)
+  return r;
+}
+#undef SSM_PICK
 
 // Staging of a backward block (kCK steps x 64 channels) by the 512 threads:
 // thread -> column scol, rows srow0 + k*8, k < 2.
@@ -671,8 +704,11 @@ struct BwdStage {
 // sums of dB, dC, dA, dD (and of a broadcast ddelta).
 // SPL: states per lane (N <= 8 * SPL).  EPI: the gate and the reverse skip.
 // BC: delta is (B,L,1), shared by the channels.
+// Rows of p0 below rows0, rows of p1 above, as ssm_fwd_kernel.
 template <int SPL, bool EPI, bool BC, typename T>
-__global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T> p) {
+__global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T> p0, BwdArgs<T> p1, int rows0) {
+  const bool second = (int)blockIdx.y >= rows0;
+  const BwdArgs<T> p = pick_args<T>(p0, p1, second);
   constexpr int NS = 8 * SPL;
   constexpr int NT = BwdStage::NT, RPT = BwdStage::RPT, RSTEP = BwdStage::RSTEP;
   constexpr int BCN = kCK * NS;
@@ -685,7 +721,7 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 7;
   const int g = lane >> 3;
-  const int b = blockIdx.y;
+  const int b = second ? (int)blockIdx.y - rows0 : (int)blockIdx.y;
   const int cb = blockIdx.x;
   const int seg = blockIdx.z;
   const int L = p.L, D = p.D, N = p.N;
@@ -780,12 +816,12 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
   const int ldy = p.ldy, ldz = p.ldz;
   const T* __restrict__ dy_b = p.dy + (int64_t)b * L * ldy;
   const T* __restrict__ z_b = EPI ? p.z + (int64_t)b * L * ldz : nullptr;
-  const T* __restrict__ B_b = p.Bc + (int64_t)b * L * N;
-  const T* __restrict__ C_b = p.Cc + (int64_t)b * L * N;
+  const int ldbc = p.ldbc;
+  const T* __restrict__ B_b = p.Bc + (int64_t)b * L * ldbc;
+  const T* __restrict__ C_b = p.Cc + (int64_t)b * L * ldbc;
   const float* __restrict__ ck_b = p.ckpt + (int64_t)b * p.nblk * N * D;
   T* __restrict__ out_b = (is_du ? p.du : p.ddelta) + (int64_t)b * L * D;  // ddelta only when (B,L,D)
   T* __restrict__ dz_b = EPI ? p.dz + (int64_t)b * L * D : nullptr;
-  const int LN = L * N;
 
   // fetch() only issues loads; commit() (after the block's compute) masks,
   // applies softplus and the gate and writes LDS
@@ -820,7 +856,7 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
       const int e = tid + k * NT;
       if (BCN % NT == 0 || e < BCN) {
         const int i = e / NS, n = e - (e / NS) * NS;
-        const uint32_t o = (uint32_t)(min((t0 + i) * N + min(n, N - 1), LN - 1) * sizeof(T));
+        const uint32_t o = (uint32_t)((min(t0 + i, L - 1) * ldbc + min(n, N - 1)) * sizeof(T));
         r_B[k] = bldr<T>(rB, o, 0);
         r_C[k] = bldr<T>(rC, o, 0);
       }
@@ -1212,8 +1248,8 @@ __device__ __forceinline__ void bwd_agg_body(const BwdArgs<T>& p, const int b) {
   const int ldy = p.ldy, ldz = p.ldz;
   const T* __restrict__ dy_b = p.dy + (int64_t)b * L * ldy;
   const T* __restrict__ z_b = EPI ? p.z + (int64_t)b * L * ldz : nullptr;
-  const T* __restrict__ C_b = p.Cc + (int64_t)b * L * N;
-  const int LN = L * N;
+  const int ldbc = p.ldbc;
+  const T* __restrict__ C_b = p.Cc + (int64_t)b * L * ldbc;
 
   const buf_t rdt = make_buf(dt_b), rdy = make_buf(dy_b), rz = make_buf(EPI ? z_b : dy_b), rC = make_buf(C_b);
   const uint32_t so_dt = (uint32_t)(scol_dt * sizeof(T)), so_q = (uint32_t)(sq * sizeof(T));
@@ -1234,7 +1270,7 @@ __device__ __forceinline__ void bwd_agg_body(const BwdArgs<T>& p, const int b) {
       const int e = tid + k * NT;
       if (BCN % NT == 0 || e < BCN) {
         const int i = e / NS, n = e - (e / NS) * NS;
-        r_C[k] = bldr<T>(rC, (uint32_t)(min((t0 + i) * N + min(n, N - 1), LN - 1) * sizeof(T)), 0);
+        r_C[k] = bldr<T>(rC, (uint32_t)((min(t0 + i, L - 1) * ldbc + min(n, N - 1)) * sizeof(T)), 0);
       }
     }
   };
@@ -1320,14 +1356,17 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_agg_kernel(BwdArg
   else bwd_agg_body<SPL, EPI, T>(p1, y - rows0);
 }
 
-// out[i] = sum_k ws[k*count + i], k = 0..nparts-1 in order.  Each thread sums
-// 4 consecutive outputs with 8 parts' loads in flight; V4 (count a multiple of
-// 4, ws 16-byte aligned) loads them as float4.
+// out[i] = sum_k ws[k*count + i], k = 0..nparts-1 in order, with element i of
+// the dense sums stored at row i / w, column i % w of an output whose rows are
+// ld elements apart (w = ld: dense).  Each thread sums 4 consecutive outputs
+// with 8 parts' loads in flight; V4 (count and w multiples of 4, ws 16-byte
+// aligned) loads them as float4.
 template <typename TO, bool V4>
 __global__ void reduce_parts_kernel(const float* __restrict__ ws, TO* __restrict__ out, int nparts,
-                                    int64_t count) {
+                                    int64_t count, int64_t w, int64_t ld) {
   const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (i0 >= count) return;
+  auto oidx = [&](int64_t i) { return w == ld ? i : (i / w) * ld + i % w; };
   constexpr int kIn = 8;
   if constexpr (V4) {
     float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -1346,14 +1385,15 @@ __global__ void reduce_parts_kernel(const float* __restrict__ ws, TO* __restrict
       for (int j = 0; j < kIn; ++j) add(v[j]);
     }
     for (; k < nparts; ++k) add(*reinterpret_cast<const float4*>(ws + (int64_t)k * count + i0));
+    const int64_t o = oidx(i0);  // the 4 stay in one row (w % 4 == 0)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) st(out, i0 + e, s[e]);
+    for (int e = 0; e < 4; ++e) st(out, o + e, s[e]);
   } else {
     const int m = (int)(count - i0 < 4 ? count - i0 : 4);
     for (int e = 0; e < m; ++e) {
       float sum = 0.0f;
       for (int k = 0; k < nparts; ++k) sum += ws[(int64_t)k * count + i0 + e];
-      st(out, i0 + e, sum);
+      st(out, oidx(i0 + e), sum);
     }
   }
 }
@@ -1366,6 +1406,7 @@ struct Shape {
   bool epi;                   // skip / gate epilogue fused
   int seg_len, nseg;          // time segments per row
   int ldy, ldz;               // row strides of y / dy and of z
+  int ldbc;                   // row stride of B, C, dB, dC
 };
 
 // Automatic time split: a row is split only when the unsplit backward grid
@@ -1415,6 +1456,8 @@ int validate(const ssm_desc_t* desc, Shape* s) {
   if ((desc->ld_y != 0 && desc->seqlen * desc->ld_y > (int64_t(1) << 30)) ||
       (desc->ld_z != 0 && desc->seqlen * desc->ld_z > (int64_t(1) << 30)))
     return fail(SSM_ERR_INVALID, "seqlen*ld_y and seqlen*ld_z must be <= 2^30");
+  if (desc->ld_bc != 0 && (desc->ld_bc < desc->dstate || desc->seqlen * desc->ld_bc > (int64_t(1) << 30)))
+    return fail(SSM_ERR_INVALID, "ld_bc must be 0 or >= dstate, with seqlen*ld_bc <= 2^30");
   s->B = (int)desc->batch;
   s->L = (int)desc->seqlen;
   s->D = (int)desc->dim;
@@ -1422,6 +1465,7 @@ int validate(const ssm_desc_t* desc, Shape* s) {
   s->ncb = (s->D + kBlkCh - 1) / kBlkCh;
   s->ldy = desc->ld_y ? (int)desc->ld_y : s->D;
   s->ldz = desc->ld_z ? (int)desc->ld_z : s->D;
+  s->ldbc = desc->ld_bc ? (int)desc->ld_bc : s->N;
   s->nblk = (s->L + kCK - 1) / kCK;
   // extra epilogue staging: the gate, and the reverse skip's u at the mirrored position
   s->epi = (desc->flags & SSM_GATE) || ((desc->flags & SSM_SKIP) && (desc->flags & SSM_REVERSE));
@@ -1495,9 +1539,17 @@ FwdArgs<T> fwd_args(const ssm_desc_t* desc, const Shape& s, const void* u, const
   a.nseg = s.nseg;
   a.ldy = s.ldy;
   a.ldz = s.ldz;
+  a.ldbc = s.ldbc;
   a.dstride = desc->delta_broadcast ? 0 : 1;
   a.flags = desc->flags;
   return a;
+}
+
+// u and delta rows read as aligned 4-element vectors (the forward's VEC variant)
+template <typename T>
+bool fwd_vec(const ssm_desc_t* desc, const Shape& s, const FwdArgs<T>& a) {
+  return s.D % 4 == 0 && !desc->delta_broadcast && reinterpret_cast<uintptr_t>(a.u) % (4 * sizeof(T)) == 0 &&
+         reinterpret_cast<uintptr_t>(a.delta) % (4 * sizeof(T)) == 0;
 }
 
 // Aggregates of every segment but the last (s.nseg > 1): rows of a0, and with
@@ -1517,28 +1569,34 @@ int launch_fwd_agg(hipStream_t st, const Shape& s, const FwdArgs<T>& a0, const F
   return hip_check(hipGetLastError(), "ssm_fwd aggregate launch");
 }
 
+// The main forward pass over rows of a0, and with a pair (rows = 2 * s.B) the
+// rows of a1 in the same launch (same shape and kernel variant).
 template <typename T>
-int launch_fwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const FwdArgs<T>& a, bool with_agg) {
-  if (with_agg && s.nseg > 1)
-    if (int rc = launch_fwd_agg<T>(st, s, a, a, s.B)) return rc;
-  const bool vec = s.D % 4 == 0 && !desc->delta_broadcast && reinterpret_cast<uintptr_t>(a.u) % (4 * sizeof(T)) == 0 &&
-                   reinterpret_cast<uintptr_t>(a.delta) % (4 * sizeof(T)) == 0;
+int launch_fwd_main(hipStream_t st, const Shape& s, const FwdArgs<T>& a0, const FwdArgs<T>& a1, int rows,
+                    bool vec) {
   if (!dispatch_spl<4, 8>(s.spl_f, s.epi, [&](auto spl, auto epi) {
         constexpr int S = decltype(spl)::value;
         constexpr bool E = decltype(epi)::value;
         auto go = [&](auto sp) {
           constexpr bool SP = decltype(sp)::value;
           if (vec)
-            hipLaunchKernelGGL((ssm_fwd_kernel<S, E, SP, true, T>), dim3(s.ncb, s.B, s.nseg),
-                               dim3(kWave * kFwdWaves), 0, st, a);
+            hipLaunchKernelGGL((ssm_fwd_kernel<S, E, SP, true, T>), dim3(s.ncb, rows, s.nseg),
+                               dim3(kWave * kFwdWaves), 0, st, a0, a1, s.B);
           else
-            hipLaunchKernelGGL((ssm_fwd_kernel<S, E, SP, false, T>), dim3(s.ncb, s.B, s.nseg),
-                               dim3(kWave * kFwdWaves), 0, st, a);
+            hipLaunchKernelGGL((ssm_fwd_kernel<S, E, SP, false, T>), dim3(s.ncb, rows, s.nseg),
+                               dim3(kWave * kFwdWaves), 0, st, a0, a1, s.B);
         };
-        if (desc->flags & SSM_DELTA_SOFTPLUS) go(std::true_type{}); else go(std::false_type{});
+        if (a0.flags & SSM_DELTA_SOFTPLUS) go(std::true_type{}); else go(std::false_type{});
       }))
     return fail(SSM_ERR_UNSUPPORTED, "no kernel variant for this shape");
   return hip_check(hipGetLastError(), "ssm_fwd launch");
+}
+
+template <typename T>
+int launch_fwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const FwdArgs<T>& a) {
+  if (s.nseg > 1)
+    if (int rc = launch_fwd_agg<T>(st, s, a, a, s.B)) return rc;
+  return launch_fwd_main<T>(st, s, a, a, s.B, fwd_vec<T>(desc, s, a));
 }
 
 template <typename T>
@@ -1578,6 +1636,7 @@ BwdArgs<T> bwd_args(const ssm_desc_t* desc, const Shape& s, const void* u, const
   a.nseg = s.nseg;
   a.ldy = s.ldy;
   a.ldz = s.ldz;
+  a.ldbc = s.ldbc;
   a.dstride = bcast ? 0 : 1;
   a.flags = desc->flags;
   return a;
@@ -1597,45 +1656,62 @@ int launch_bwd_agg(hipStream_t st, const Shape& s, const BwdArgs<T>& a0, const B
   return hip_check(hipGetLastError(), "ssm_bwd aggregate launch");
 }
 
+// The main backward pass over rows of a0, and with a pair (rows = 2 * s.B) the
+// rows of a1 in the same launch (same shape and kernel variant).
 template <typename T>
-int launch_bwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const BwdArgs<T>& a, float* dA, void* dB,
-               void* dC, float* dD, void* ddelta, void* workspace, bool with_agg) {
-  const bool bcast = desc->delta_broadcast != 0;
-  const WsLayout wl = ws_layout(s, bcast);
-  float* ws = static_cast<float*>(workspace);
-  if (with_agg && s.nseg > 1)
-    if (int rc = launch_bwd_agg<T>(st, s, a, a, s.B)) return rc;
+int launch_bwd_main(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const BwdArgs<T>& a0,
+                    const BwdArgs<T>& a1, int rows) {
   if (!dispatch_spl<2, 4>(s.spl_b, s.epi, [&](auto spl, auto epi) {
         constexpr int S = decltype(spl)::value;
         constexpr bool E = decltype(epi)::value;
         if (desc->delta_broadcast)
-          hipLaunchKernelGGL((ssm_bwd_kernel<S, E, true, T>), dim3(s.ncb, s.B, s.nseg), dim3(kWave * kBwdWaves), 0,
-                             st, a);
+          hipLaunchKernelGGL((ssm_bwd_kernel<S, E, true, T>), dim3(s.ncb, rows, s.nseg), dim3(kWave * kBwdWaves), 0,
+                             st, a0, a1, s.B);
         else
-          hipLaunchKernelGGL((ssm_bwd_kernel<S, E, false, T>), dim3(s.ncb, s.B, s.nseg), dim3(kWave * kBwdWaves), 0,
-                             st, a);
+          hipLaunchKernelGGL((ssm_bwd_kernel<S, E, false, T>), dim3(s.ncb, rows, s.nseg), dim3(kWave * kBwdWaves), 0,
+                             st, a0, a1, s.B);
       }))
     return fail(SSM_ERR_UNSUPPORTED, "no kernel variant for this shape");
-  int rc = hip_check(hipGetLastError(), "ssm_bwd launch");
-  if (rc) return rc;
-  auto reduce = [&](const float* part, auto* out, int nparts, int64_t count) {
+  return hip_check(hipGetLastError(), "ssm_bwd launch");
+}
+
+// The fixed-order reductions of a backward's partial sums into dB, dC, dA, dD
+// (and a broadcast delta's gradient).
+template <typename T>
+int launch_bwd_reduce(hipStream_t st, const ssm_desc_t* desc, const Shape& s, float* dA, void* dB, void* dC,
+                      float* dD, void* ddelta, void* workspace) {
+  const bool bcast = desc->delta_broadcast != 0;
+  const WsLayout wl = ws_layout(s, bcast);
+  float* ws = static_cast<float*>(workspace);
+  auto reduce = [&](const float* part, auto* out, int nparts, int64_t count, int64_t w, int64_t ld) {
     using TO = std::remove_pointer_t<decltype(out)>;
     const int threads = 256;
     const int64_t blocks = ((count + 3) / 4 + threads - 1) / threads;
-    if (count % 4 == 0 && reinterpret_cast<uintptr_t>(part) % 16 == 0)
+    if (count % 4 == 0 && w % 4 == 0 && reinterpret_cast<uintptr_t>(part) % 16 == 0)
       hipLaunchKernelGGL((reduce_parts_kernel<TO, true>), dim3((unsigned)blocks), dim3(threads), 0, st, part,
-                         out, nparts, count);
+                         out, nparts, count, w, ld);
     else
       hipLaunchKernelGGL((reduce_parts_kernel<TO, false>), dim3((unsigned)blocks), dim3(threads), 0, st, part,
-                         out, nparts, count);
+                         out, nparts, count, w, ld);
   };
   const int64_t bln = (int64_t)s.B * s.L * s.N;
-  reduce(ws + wl.dB, static_cast<T*>(dB), s.ncb, bln);
-  reduce(ws + wl.dC, static_cast<T*>(dC), s.ncb, bln);
-  reduce(ws + wl.dA, dA, s.B * s.nseg, (int64_t)s.D * s.N);
-  if (desc->flags & SSM_SKIP) reduce(ws + wl.dD, dD, s.B * s.nseg, (int64_t)s.D);
-  if (bcast) reduce(ws + wl.ddt, static_cast<T*>(ddelta), s.ncb, (int64_t)s.B * s.L);
+  const int64_t dn = (int64_t)s.D * s.N;
+  const int64_t bl = (int64_t)s.B * s.L;
+  reduce(ws + wl.dB, static_cast<T*>(dB), s.ncb, bln, s.N, s.ldbc);
+  reduce(ws + wl.dC, static_cast<T*>(dC), s.ncb, bln, s.N, s.ldbc);
+  reduce(ws + wl.dA, dA, s.B * s.nseg, dn, dn, dn);
+  if (desc->flags & SSM_SKIP) reduce(ws + wl.dD, dD, s.B * s.nseg, (int64_t)s.D, s.D, s.D);
+  if (bcast) reduce(ws + wl.ddt, static_cast<T*>(ddelta), s.ncb, bl, bl, bl);
   return hip_check(hipGetLastError(), "ssm_bwd reduce launch");
+}
+
+template <typename T>
+int launch_bwd(hipStream_t st, const ssm_desc_t* desc, const Shape& s, const BwdArgs<T>& a, float* dA, void* dB,
+               void* dC, float* dD, void* ddelta, void* workspace) {
+  if (s.nseg > 1)
+    if (int rc = launch_bwd_agg<T>(st, s, a, a, s.B)) return rc;
+  if (int rc = launch_bwd_main<T>(st, desc, s, a, a, s.B)) return rc;
+  return launch_bwd_reduce<T>(st, desc, s, dA, dB, dC, dD, ddelta, workspace);
 }
 
 }  // namespace
@@ -1732,10 +1808,8 @@ int ssm_fwd(void* stream, const ssm_desc_t* desc, const void* u, const void* del
   if ((desc->flags & SSM_GATE) && !z) return fail(SSM_ERR_INVALID, "SSM_GATE needs z");
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (desc->dtype == SSM_F32)
-    return launch_fwd<float>(st, desc, s, fwd_args<float>(desc, s, u, delta, A, Bc, Cc, Dskip, z, y, ckpt, workspace),
-                             true);
-  return launch_fwd<bf16>(st, desc, s, fwd_args<bf16>(desc, s, u, delta, A, Bc, Cc, Dskip, z, y, ckpt, workspace),
-                          true);
+    return launch_fwd<float>(st, desc, s, fwd_args<float>(desc, s, u, delta, A, Bc, Cc, Dskip, z, y, ckpt, workspace));
+  return launch_fwd<bf16>(st, desc, s, fwd_args<bf16>(desc, s, u, delta, A, Bc, Cc, Dskip, z, y, ckpt, workspace));
 }
 
 int ssm_bwd(void* stream, const ssm_desc_t* desc, const void* u, const void* delta, const float* A,
@@ -1752,10 +1826,10 @@ int ssm_bwd(void* stream, const ssm_desc_t* desc, const void* u, const void* del
   if (desc->dtype == SSM_F32)
     return launch_bwd<float>(st, desc, s,
                              bwd_args<float>(desc, s, u, delta, A, Bc, Cc, Dskip, z, ckpt, dy, du, ddelta, dz, workspace),
-                             dA, dB, dC, dD, ddelta, workspace, true);
+                             dA, dB, dC, dD, ddelta, workspace);
   return launch_bwd<bf16>(st, desc, s,
                           bwd_args<bf16>(desc, s, u, delta, A, Bc, Cc, Dskip, z, ckpt, dy, du, ddelta, dz, workspace),
-                          dA, dB, dC, dD, ddelta, workspace, true);
+                          dA, dB, dC, dD, ddelta, workspace);
 }
 
 int ssm_bwd_static(void* stream, const ssm_desc_t* desc, const void* u, const void* delta, const float* A,
@@ -1782,10 +1856,11 @@ int ssm_bwd_static(void* stream, const ssm_desc_t* desc, const void* u, const vo
   return ssm_bwd(stream, desc, u, delta, A, Bc, Cc, Dskip, z, ckpt, dy, du, ddelta, dA, dB, dC, dD, dz, ws);
 }
 
-// The two calls of a pair as ssm_fwd / ssm_bwd would make them, with the
-// time-split aggregate passes of both in one launch when the two descs have
-// the same shape and kernel variant (each keeps its own segments, so the
-// results equal two separate calls bit for bit).
+// The two calls of a pair as ssm_fwd / ssm_bwd would make them.  When the two
+// descs have the same shape, their time-split aggregate passes share one
+// launch, and so do their main passes when they also need the same kernel
+// variant (epilogue staging, vector staging).  Each call keeps its own time
+// segments, so the results equal two separate calls bit for bit.
 static bool same_shape(const ssm_desc_t& a, const ssm_desc_t& b) {
   return a.batch == b.batch && a.seqlen == b.seqlen && a.dim == b.dim && a.dstate == b.dstate &&
          a.dtype == b.dtype && a.delta_broadcast == b.delta_broadcast && a.segments == b.segments &&
@@ -1808,18 +1883,28 @@ int ssm_fwd_pair(void* stream, const ssm_desc_t* desc, const ssm_fwd_io_t* io) {
   }
   // one element type for both calls: the kernels of a pair are chosen once
   if (desc[0].dtype != desc[1].dtype) return fail(SSM_ERR_INVALID, "ssm_fwd_pair: the two descs must have the same dtype");
-  const bool joint = same_shape(desc[0], desc[1]) && s[0].nseg > 1 && 2 * s[0].B <= kMaxGridY;
+  const bool same = same_shape(desc[0], desc[1]) && 2 * s[0].B <= kMaxGridY;
   hipStream_t st = static_cast<hipStream_t>(stream);
   auto run = [&](auto tag) -> int {
     using T = decltype(tag);
     FwdArgs<T> a[2];
-    for (int k = 0; k < 2; ++k)
+    bool vec[2];
+    for (int k = 0; k < 2; ++k) {
       a[k] = fwd_args<T>(&desc[k], s[k], io[k].u, io[k].delta, io[k].A, io[k].B, io[k].C, io[k].D, io[k].z,
                          io[k].y, io[k].ckpt, io[k].workspace);
-    if (joint)
+      vec[k] = fwd_vec<T>(&desc[k], s[k], a[k]);
+    }
+    if (same && s[0].nseg > 1) {
       if (int rc = launch_fwd_agg<T>(st, s[0], a[0], a[1], 2 * s[0].B)) return rc;
+    } else {
+      for (int k = 0; k < 2; ++k)
+        if (s[k].nseg > 1)
+          if (int rc = launch_fwd_agg<T>(st, s[k], a[k], a[k], s[k].B)) return rc;
+    }
+    if (same && s[0].epi == s[1].epi && vec[0] == vec[1])
+      return launch_fwd_main<T>(st, s[0], a[0], a[1], 2 * s[0].B, vec[0]);
     for (int k = 0; k < 2; ++k)
-      if (int rc = launch_fwd<T>(st, &desc[k], s[k], a[k], !joint)) return rc;
+      if (int rc = launch_fwd_main<T>(st, s[k], a[k], a[k], s[k].B, vec[k])) return rc;
     return SSM_OK;
   };
   return desc[0].dtype == SSM_F32 ? run(float{}) : run(bf16{});
@@ -1839,7 +1924,8 @@ int ssm_bwd_pair(void* stream, const ssm_desc_t* desc, const ssm_bwd_io_t* io) {
     if ((desc[k].flags & SSM_GATE) && (!q.z || !q.dz)) return fail(SSM_ERR_INVALID, "SSM_GATE needs z and dz");
   }
   if (desc[0].dtype != desc[1].dtype) return fail(SSM_ERR_INVALID, "ssm_bwd_pair: the two descs must have the same dtype");
-  const bool joint = same_shape(desc[0], desc[1]) && s[0].nseg > 1 && s[0].epi == s[1].epi && 2 * s[0].B <= kMaxGridY;
+  // the backward kernels' variant: the epilogue staging (and delta broadcast, part of the shape)
+  const bool same = same_shape(desc[0], desc[1]) && s[0].epi == s[1].epi && 2 * s[0].B <= kMaxGridY;
   hipStream_t st = static_cast<hipStream_t>(stream);
   auto run = [&](auto tag) -> int {
     using T = decltype(tag);
@@ -1847,11 +1933,20 @@ int ssm_bwd_pair(void* stream, const ssm_desc_t* desc, const ssm_bwd_io_t* io) {
     for (int k = 0; k < 2; ++k)
       a[k] = bwd_args<T>(&desc[k], s[k], io[k].u, io[k].delta, io[k].A, io[k].B, io[k].C, io[k].D, io[k].z,
                          io[k].ckpt, io[k].dy, io[k].du, io[k].ddelta, io[k].dz, io[k].workspace);
-    if (joint)
-      if (int rc = launch_bwd_agg<T>(st, s[0], a[0], a[1], 2 * s[0].B)) return rc;
+    if (same) {
+      if (s[0].nseg > 1)
+        if (int rc = launch_bwd_agg<T>(st, s[0], a[0], a[1], 2 * s[0].B)) return rc;
+      if (int rc = launch_bwd_main<T>(st, &desc[0], s[0], a[0], a[1], 2 * s[0].B)) return rc;
+    } else {
+      for (int k = 0; k < 2; ++k) {
+        if (s[k].nseg > 1)
+          if (int rc = launch_bwd_agg<T>(st, s[k], a[k], a[k], s[k].B)) return rc;
+        if (int rc = launch_bwd_main<T>(st, &desc[k], s[k], a[k], a[k], s[k].B)) return rc;
+      }
+    }
     for (int k = 0; k < 2; ++k)
-      if (int rc = launch_bwd<T>(st, &desc[k], s[k], a[k], io[k].dA, io[k].dB, io[k].dC, io[k].dD, io[k].ddelta,
-                                 io[k].workspace, !joint))
+      if (int rc = launch_bwd_reduce<T>(st, &desc[k], s[k], io[k].dA, io[k].dB, io[k].dC, io[k].dD, io[k].ddelta,
+                                        io[k].workspace))
         return rc;
     return SSM_OK;
   };

@@ -187,8 +187,10 @@ def _core_project(u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, N, rank):
         dt = torch.repeat_interleave(dt_low, D // rank, dim=-1).reshape(B_, L_, D)
     else:
         dt = dt_low.reshape(B_, L_, 1)
-    Bc = BC[:, :N].reshape(B_, L_, N).contiguous()
-    Cc = BC[:, N:].reshape(B_, L_, N).contiguous()
+    # B and C stay column slices of the projection's (B, L, 2N) output, which the
+    # scan reads in place (desc.ld_bc = 2N)
+    BC3 = BC.reshape(B_, L_, 2 * N)
+    Bc, Cc = BC3[..., :N], BC3[..., N:]
     A = -torch.exp(A_log)
     return A, dt_low, dt.contiguous(), Bc, Cc
 
@@ -202,28 +204,36 @@ def _core_forward(u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, Dp, z, N, rank, reverse,
     return y, (u, A, Wbc, Wdt, Wp, Dp, z, dt_low, dt, Bc, Cc, ckpt)
 
 
-def _scan_call(saved, reverse, complement):
+def _dbc_buffer(u, N):
+    """The BC projection's gradient (B, L, 2N): the scan's backward writes dB and dC
+    straight into its two column halves."""
+    return torch.empty(*u.shape[:-1], 2 * N, dtype=u.dtype, device=u.device)
+
+
+def _scan_call(saved, reverse, complement, N):
     """The scan's arguments for the scan_*_pair launchers, from _core_forward's saved tensors."""
     u, A, _, _, _, Dp, z, _, dt, Bc, Cc, ckpt = saved
     return dict(u=u, delta=dt, A=A, B=Bc, C=Cc, Dskip=Dp, z=z, reverse=reverse, complement=complement,
-                delta_softplus=True)
+                delta_softplus=True, dbc_out=_dbc_buffer(u, N))
 
 
 def _core_backward(saved, dy, N, rank, reverse, complement):
     """Gradients of _core_forward for (u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, D, z)."""
     u, A, Wbc, Wdt, Wp, Dp, z, dt_low, dt, Bc, Cc, ckpt = saved
-    grads = scan_bwd(u, dt, A, Bc, Cc, Dp, z, ckpt, dy, reverse, complement, delta_softplus=True)
-    return _core_param_grads(saved, grads, N, rank)
+    dbc = _dbc_buffer(u, N)
+    grads = scan_bwd(u, dt, A, Bc, Cc, Dp, z, ckpt, dy, reverse, complement, delta_softplus=True, dbc_out=dbc)
+    return _core_param_grads(saved, grads, dbc, N, rank)
 
 
-def _core_param_grads(saved, grads, N, rank):
-    """_core_backward after the scan's backward: the projections' and u's gradients."""
+def _core_param_grads(saved, grads, dbc, N, rank):
+    """_core_backward after the scan's backward (which wrote dB, dC into ``dbc``): the
+    projections' and u's gradients."""
     u, A, Wbc, Wdt, Wp, Dp, z, dt_low, dt, Bc, Cc, ckpt = saved
     du, ddt, dA, dB, dC, dD, dz = grads
     D = u.shape[-1]
     u2 = u.reshape(-1, D)
     du2 = du.reshape(-1, D)
-    dBC = torch.cat([dB.reshape(-1, N), dC.reshape(-1, N)], dim=1)
+    dBC = dbc.reshape(-1, 2 * N)
     dWbc = _tn(u2, dBC)
     dbbc = dBC.sum(0)
     du2.addmm_(dBC, Wbc.to(u.dtype).t())  # u's gradient through BC, accumulated in place
@@ -317,10 +327,10 @@ class _PairCoreFn(torch.autograd.Function):
         E = saved[0].shape[-1]
         dy, _ = as_rows(dy, saved[0].dtype)
         sf, sr = saved[:k], saved[k:]
-        scan_gf, scan_gr = scan_bwd_pair([dict(_scan_call(sf, False, False), ckpt=sf[-1], dy=dy[..., :E]),
-                                          dict(_scan_call(sr, True, complement), ckpt=sr[-1], dy=dy[..., E:])])
-        gf = _core_param_grads(sf, scan_gf, N, rank)
-        gr = _core_param_grads(sr, scan_gr, N, rank)
+        cf, cr = _scan_call(sf, False, False, N), _scan_call(sr, True, complement, N)
+        scan_gf, scan_gr = scan_bwd_pair([dict(cf, ckpt=sf[-1], dy=dy[..., :E]), dict(cr, ckpt=sr[-1], dy=dy[..., E:])])
+        gf = _core_param_grads(sf, scan_gf, cf["dbc_out"], N, rank)
+        gr = _core_param_grads(sr, scan_gr, cr["dbc_out"], N, rank)
         return (*gf, *gr, None, None, None, None)
 
 

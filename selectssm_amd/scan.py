@@ -109,10 +109,11 @@ def _flags(skip, gate, reverse, complement, delta_softplus=False):
     return f
 
 
-def _desc(u, delta, A, flags, segments=0, ld_y=0, ld_z=0):
+def _desc(u, delta, A, flags, segments=0, ld_y=0, ld_z=0, ld_bc=0):
     Bt, Ln, D = u.shape
     return L.make_desc(Bt, Ln, D, A.shape[1], _IO_DTYPES[u.dtype], flags,
-                       delta_broadcast=(delta.shape[-1] == 1 and D != 1), segments=segments, ld_y=ld_y, ld_z=ld_z)
+                       delta_broadcast=(delta.shape[-1] == 1 and D != 1), segments=segments, ld_y=ld_y, ld_z=ld_z,
+                       ld_bc=ld_bc)
 
 
 def row_stride(t):
@@ -146,6 +147,46 @@ def needs_grad(*ts) -> bool:
     return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
 
 
+def bc_stride(B, C):
+    """The common row stride of B and C (:func:`row_stride`), which the kernels take
+    as desc.ld_bc: B and C may be column slices of one wider array, e.g. of the BC
+    projection's output.  Raises if they are not both readable in place with one stride."""
+    ld_b, ld_c = row_stride(B), row_stride(C)
+    if ld_b is None or ld_c is None or ld_b != ld_c:
+        raise ValueError("B and C must be contiguous or column slices with one row stride of a contiguous "
+                         "(B, L, W) tensor")
+    return ld_b
+
+
+def bc_rows(B, C, dtype):
+    """B and C in ``dtype`` as views the kernels read in place (one row stride), copying
+    both to contiguous arrays only if they are not."""
+    if B.dtype == dtype and C.dtype == dtype:
+        ld_b, ld_c = row_stride(B), row_stride(C)
+        if ld_b is not None and ld_b == ld_c:
+            return B, C
+    return B.to(dtype).contiguous(), C.to(dtype).contiguous()
+
+
+def _bc_grads(B, C, ld_bc, dbc_out):
+    """Output arrays for dB and dC with the row stride ld_bc of B and C: two column
+    slices of ``dbc_out`` ((B, L, W) with W = ld_bc >= 2N: dB in columns [0, N),
+    dC in [N, 2N)), of a new such array, or two new arrays."""
+    N = B.shape[-1]
+    if ld_bc == N:
+        return torch.empty_like(B), torch.empty_like(C)
+    shape = (*B.shape[:-1], ld_bc)
+    if dbc_out is not None:
+        if tuple(dbc_out.shape) != shape or not dbc_out.is_contiguous() or dbc_out.dtype != B.dtype:
+            raise ValueError(f"dbc_out must be a contiguous {B.dtype} array of shape {shape}")
+        return dbc_out[..., :N], dbc_out[..., N:2 * N]
+    if ld_bc >= 2 * N:
+        buf = torch.empty(shape, dtype=B.dtype, device=B.device)
+        return buf[..., :N], buf[..., N:2 * N]
+    return (torch.empty(shape, dtype=B.dtype, device=B.device)[..., :N],
+            torch.empty(shape, dtype=C.dtype, device=C.device)[..., :N])
+
+
 def _scratch(nbytes, device):
     return torch.empty(nbytes // 4, dtype=torch.float32, device=device) if nbytes else None
 
@@ -159,7 +200,8 @@ def scan_fwd(u, delta, A, B, C, Dskip=None, z=None, reverse=False, complement=Fa
 
     ``segments`` splits each row's time axis (0: chosen from the shape);
     ``delta_softplus``: ``delta`` is the pre-activation and the scan uses
-    softplus(delta); ``y_out``: where to write y (allocated if None).
+    softplus(delta); ``y_out``: where to write y (allocated if None).  B and C
+    may be column slices of one array (:func:`bc_stride`).
     Returns ``(y, ckpt)``; ``ckpt`` is None when ``want_ckpt`` is False.
     """
     flags = _flags(Dskip is not None, z is not None, reverse, complement, delta_softplus)
@@ -167,7 +209,7 @@ def scan_fwd(u, delta, A, B, C, Dskip=None, z=None, reverse=False, complement=Fa
     ld_y, ld_z = row_stride(y), (row_stride(z) if z is not None else 0)
     if ld_y is None or ld_z is None:
         raise ValueError("y_out and z must be contiguous or column slices of a contiguous (B, L, W) tensor")
-    desc = _desc(u, delta, A, flags, segments, ld_y=ld_y, ld_z=ld_z)
+    desc = _desc(u, delta, A, flags, segments, ld_y=ld_y, ld_z=ld_z, ld_bc=bc_stride(B, C))
     lib = L.lib()
     ckpt = _scratch(L.size_query(lib.ssm_ckpt_bytes, desc), u.device) if want_ckpt else None
     ws = _scratch(L.size_query(lib.ssm_fwd_workspace_bytes, desc, allow_zero=True), u.device)
@@ -177,21 +219,23 @@ def scan_fwd(u, delta, A, B, C, Dskip=None, z=None, reverse=False, complement=Fa
 
 
 def scan_bwd(u, delta, A, B, C, Dskip, z, ckpt, dy, reverse=False, complement=False, segments=0,
-             delta_softplus=False):
+             delta_softplus=False, dbc_out=None):
     """Run ``ssm_bwd``.  Returns ``(du, ddelta, dA, dB, dC, dD, dz)`` (dD / dz None when unused);
     with ``delta_softplus``, ``ddelta`` is the gradient w.r.t. the pre-activation.
-    ``dy`` and ``z`` may be row-strided column slices; dz is always contiguous."""
+    ``dy`` and ``z`` may be row-strided column slices; dz is always contiguous.  When
+    B and C are column slices of one array, dB and dC are the matching slices of
+    ``dbc_out`` (or of a new array of that width)."""
     flags = _flags(Dskip is not None, z is not None, reverse, complement, delta_softplus)
     ld_y, ld_z = row_stride(dy), (row_stride(z) if z is not None else 0)
     if ld_y is None or ld_z is None:
         raise ValueError("dy and z must be contiguous or column slices of a contiguous (B, L, W) tensor")
-    desc = _desc(u, delta, A, flags, segments, ld_y=ld_y, ld_z=ld_z)
+    ld_bc = bc_stride(B, C)
+    desc = _desc(u, delta, A, flags, segments, ld_y=ld_y, ld_z=ld_z, ld_bc=ld_bc)
     lib = L.lib()
     du = torch.empty_like(u)
     ddelta = torch.empty_like(delta)
     dA = torch.empty_like(A)
-    dB = torch.empty_like(B)
-    dC = torch.empty_like(C)
+    dB, dC = _bc_grads(B, C, ld_bc, dbc_out)
     dD = torch.empty_like(Dskip) if Dskip is not None else None
     dz = torch.empty_like(z) if z is not None else None
     ws = _scratch(L.size_query(lib.ssm_bwd_workspace_bytes, desc), u.device)
@@ -219,7 +263,7 @@ def scan_fwd_pair(calls):
         ld_y, ld_z = row_stride(y), (row_stride(z) if z is not None else 0)
         if ld_y is None or ld_z is None:
             raise ValueError("y_out and z must be contiguous or column slices of a contiguous (B, L, W) tensor")
-        descs[k] = _desc(u, delta, A, flags, c.get("segments", 0), ld_y=ld_y, ld_z=ld_z)
+        descs[k] = _desc(u, delta, A, flags, c.get("segments", 0), ld_y=ld_y, ld_z=ld_z, ld_bc=bc_stride(B, C))
         ckpt = (_scratch(L.size_query(lib.ssm_ckpt_bytes, descs[k]), u.device) if c.get("want_ckpt", True)
                 else None)
         ws = _scratch(L.size_query(lib.ssm_fwd_workspace_bytes, descs[k], allow_zero=True), u.device)
@@ -232,7 +276,8 @@ def scan_fwd_pair(calls):
 
 def scan_bwd_pair(calls):
     """Run ``ssm_bwd_pair``: two :func:`scan_bwd` calls, given as dicts of its
-    keyword arguments (``u, delta, A, B, C, Dskip, z, ckpt, dy`` and the flags).
+    keyword arguments (``u, delta, A, B, C, Dskip, z, ckpt, dy``, the flags and
+    optionally ``dbc_out``).
     Returns the two ``(du, ddelta, dA, dB, dC, dD, dz)`` tuples."""
     if len(calls) != 2:
         raise ValueError("scan_bwd_pair takes two calls")
@@ -246,9 +291,10 @@ def scan_bwd_pair(calls):
         ld_y, ld_z = row_stride(dy), (row_stride(z) if z is not None else 0)
         if ld_y is None or ld_z is None:
             raise ValueError("dy and z must be contiguous or column slices of a contiguous (B, L, W) tensor")
-        descs[k] = _desc(u, delta, A, flags, c.get("segments", 0), ld_y=ld_y, ld_z=ld_z)
-        g = (torch.empty_like(u), torch.empty_like(delta), torch.empty_like(A), torch.empty_like(B),
-             torch.empty_like(C), torch.empty_like(Dskip) if Dskip is not None else None,
+        ld_bc = bc_stride(B, C)
+        descs[k] = _desc(u, delta, A, flags, c.get("segments", 0), ld_y=ld_y, ld_z=ld_z, ld_bc=ld_bc)
+        g = (torch.empty_like(u), torch.empty_like(delta), torch.empty_like(A),
+             *_bc_grads(B, C, ld_bc, c.get("dbc_out")), torch.empty_like(Dskip) if Dskip is not None else None,
              torch.empty_like(z) if z is not None else None)
         ws = _scratch(L.size_query(lib.ssm_bwd_workspace_bytes, descs[k]), u.device)
         ios[k] = L.SsmBwdIo(_ptr(u), _ptr(delta), _ptr(A), _ptr(B), _ptr(C), _ptr(Dskip), _ptr(z), _ptr(c["ckpt"]),
@@ -313,7 +359,8 @@ def selective_scan(u, delta, A, B, C, D=None, z=None, reverse=False, complement=
     fcast = lambda t: None if t is None else t.to(torch.float32).contiguous()
     if not 0 <= int(segments) <= 1024:
         raise ValueError(f"segments must be in 0..1024, got {segments}")
-    return SelectiveScanFn.apply(cast(u), cast(delta), fcast(A), cast(B), cast(C), fcast(D), as_rows(z, io)[0],
+    Bk, Ck = bc_rows(B, C, io)
+    return SelectiveScanFn.apply(cast(u), cast(delta), fcast(A), Bk, Ck, fcast(D), as_rows(z, io)[0],
                                  bool(reverse), bool(complement), int(segments), bool(delta_softplus),
                                  needs_grad(u, delta, A, B, C, D, z))
 
@@ -364,7 +411,7 @@ def bidirectional_selective_scan(fwd, rev, complement=False, delta_softplus=Fals
     args = []
     for d in (fwd, rev):
         _check_shapes(d["u"], d["delta"], d["A"], d["B"], d["C"], d.get("D"), d.get("z"))
-        args += [cast(d["u"]), cast(d["delta"]), fcast(d["A"]), cast(d["B"]), cast(d["C"]), fcast(d.get("D")),
+        args += [cast(d["u"]), cast(d["delta"]), fcast(d["A"]), *bc_rows(d["B"], d["C"], io), fcast(d.get("D")),
                  as_rows(d.get("z"), io)[0]]
     if fwd["u"].shape != rev["u"].shape:
         raise ValueError("the two directions must have the same (B, L, D)")

@@ -38,7 +38,7 @@ def test_header_constants_match_binding():
     assert int(consts["SSM_ABI_VERSION"]) == L.ABI_VERSION
     m = re.search(r"#define SSM_STATIC_SCRATCH_BYTES \((\d+)u << (\d+)\)", text)
     assert m and int(m[1]) << int(m[2]) == L.STATIC_SCRATCH_BYTES
-    assert ctypes.sizeof(L.SsmDesc) == 64
+    assert ctypes.sizeof(L.SsmDesc) == 72
 
 
 def test_size_queries():
@@ -91,7 +91,7 @@ def test_split_forward_needs_its_workspace():
     ("batch", 0, b"batch, seqlen and dim"), ("dstate", 0, b"dstate"), ("dtype", 7, b"dtype"),
     ("flags", 32, b"unknown flag"), ("flags", 2, b"COMPLEMENT requires"), ("delta_broadcast", 3, b"delta_broadcast"),
     ("segments", -1, b"segments"), ("segments", 1025, b"segments"), ("ld_y", 63, b"ld_y"), ("ld_z", 1, b"ld_z"),
-    ("ld_y", 1 << 28, b"seqlen*ld_y"),
+    ("ld_y", 1 << 28, b"seqlen*ld_y"), ("ld_bc", 15, b"ld_bc"), ("ld_bc", 1 << 28, b"ld_bc"),
 ])
 def test_invalid_desc_is_rejected_before_any_launch(field, value, msg):
     lib = L.lib()

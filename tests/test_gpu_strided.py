@@ -118,3 +118,93 @@ def test_bidirectional_mamba_pair_path_equals_per_direction_path():
         # weight gradients are sums over B*L terms, so compare at their scale
         ref = pb[k].grad
         assert torch.allclose(pa[k].grad, ref, rtol=1e-4, atol=1e-5 * float(ref.abs().max())), k
+
+
+@pytest.mark.parametrize("dtype,width,segments,flags", [
+    (torch.float32, 2, 0, ()),
+    (torch.float32, 3, 3, ("gate", "skip", "reverse", "complement", "softplus")),
+    (torch.bfloat16, 2, 2, ("gate", "skip")),
+], ids=lambda v: str(v))
+def test_scan_reads_bc_in_place_and_writes_dbc(dtype, width, segments, flags):
+    """B and C read as column slices of one (B, L, width*N) array (the BC projection's
+    output, desc.ld_bc), and dB, dC written into the matching slices of one gradient
+    array: bitwise the results on contiguous B, C, dB, dC."""
+    from selectssm_amd.scan import bc_stride, scan_bwd, scan_fwd
+
+    x = make_inputs_gpu(2, 333, 72, 16, seed=7)
+    io = {k: x[k].to(dtype).contiguous() for k in ("u", "dt", "B", "C", "z", "g")}
+    N = 16
+    bc = torch.randn(2, 333, width * N, device="cuda").to(dtype)
+    bc[..., :N] = io["B"]
+    bc[..., N:2 * N] = io["C"]
+    Bs, Cs = bc[..., :N], bc[..., N:2 * N]
+    assert bc_stride(Bs, Cs) == width * N
+    rev, comp = "reverse" in flags, "complement" in flags
+    D = x["D"] if "skip" in flags else None
+    z = io["z"] if "gate" in flags else None
+    kw = dict(segments=segments, delta_softplus="softplus" in flags)
+    y0, ck0 = scan_fwd(io["u"], io["dt"], x["A"], io["B"], io["C"], D, z, rev, comp, **kw)
+    y1, ck1 = scan_fwd(io["u"], io["dt"], x["A"], Bs, Cs, D, z, rev, comp, **kw)
+    assert torch.equal(y0, y1) and torch.equal(ck0, ck1)
+    g0 = scan_bwd(io["u"], io["dt"], x["A"], io["B"], io["C"], D, z, ck0, io["g"], rev, comp, **kw)
+    dbc = torch.full((2, 333, width * N), 5.0, device="cuda", dtype=dtype)
+    g1 = scan_bwd(io["u"], io["dt"], x["A"], Bs, Cs, D, z, ck0, io["g"], rev, comp, dbc_out=dbc, **kw)
+    for a, b in zip(g0, g1):
+        assert (a is None and b is None) or torch.equal(a, b)
+    assert torch.equal(dbc[..., :N], g0[3]) and torch.equal(dbc[..., N:2 * N], g0[4])
+    assert torch.equal(dbc[..., 2 * N:], torch.full_like(dbc[..., 2 * N:], 5.0))  # columns beyond 2N untouched
+    # the pair entry points with both calls reading B, C in place (one joint launch per kernel)
+    from selectssm_amd.scan import scan_bwd_pair, scan_fwd_pair
+
+    calls = [dict(u=io["u"], delta=io["dt"], A=x["A"], B=Bs, C=Cs, Dskip=D, z=z, **kw),
+             dict(u=io["u"], delta=io["dt"], A=(x["A"] * 0.5).contiguous(), B=Bs, C=Cs, Dskip=D, z=z,
+                  reverse=True, complement=True, **kw)]
+    pair = scan_fwd_pair(calls)
+    single = [scan_fwd(**dict(c, B=io["B"], C=io["C"])) for c in calls]
+    for (yp, cp), (ys, cs) in zip(pair, single):
+        assert torch.equal(yp, ys) and torch.equal(cp, cs)
+    pg = scan_bwd_pair([dict(c, ckpt=ck, dy=io["g"]) for c, (_, ck) in zip(calls, pair)])
+    for c, (_, ck), gp in zip(calls, single, pg):
+        gs = scan_bwd(**dict(dict(Dskip=None, z=None), **dict(c, B=io["B"], C=io["C"])), ckpt=ck, dy=io["g"])
+        for a, b in zip(gs, gp):
+            assert (a is None and b is None) or torch.equal(a, b)
+
+
+def test_module_bc_projection_read_in_place_matches_copies(monkeypatch):
+    """SelectiveSSM passes B, C as slices of the BC projection output and receives dB, dC
+    in one (B, L, 2N) gradient: the same module with B, C copied to contiguous arrays
+    (and dB, dC concatenated) gives the same output and parameter gradients bit for bit."""
+    from selectssm_amd import SelectiveSSM, modules
+
+    g = torch.Generator(device="cuda").manual_seed(9)
+    m = SelectiveSSM(hidden_features=16, shift_conv_size=4, features=96, device="cuda", generator=g)
+    x = torch.randn(2, 700, 96, device="cuda", generator=g)
+    dy = torch.randn(2, 700, 96, device="cuda", generator=g)
+
+    def run():
+        for p in m.parameters():
+            p.grad = None
+        xx = x.clone().requires_grad_(True)
+        y = m(xx)
+        y.backward(dy)
+        return y.detach(), xx.grad, {k: p.grad.clone() for k, p in m.named_parameters()}
+
+    ref = run()
+    orig = modules._core_project
+
+    def copying(*a, **k):
+        A, dt_low, dt, Bc, Cc = orig(*a, **k)
+        return A, dt_low, dt, Bc.contiguous(), Cc.contiguous()
+
+    monkeypatch.setattr(modules, "_core_project", copying)
+    orig_grads = modules._core_param_grads
+
+    def cat_grads(saved, grads, dbc, N, rank):
+        du, ddt, dA, dB, dC, dD, dz = grads
+        return orig_grads(saved, grads, torch.cat([dB, dC], dim=-1), N, rank)
+
+    monkeypatch.setattr(modules, "_core_param_grads", cat_grads)
+    got = run()
+    assert torch.equal(ref[0], got[0]) and torch.equal(ref[1], got[1])
+    for k in ref[2]:
+        assert torch.equal(ref[2][k], got[2][k]), k
