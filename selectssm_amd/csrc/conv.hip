@@ -243,6 +243,10 @@ int validate_conv(const ssm_conv_desc_t* desc, ConvShape* s) {
   if (desc->batch < 1 || desc->seqlen < 1 || desc->dim < 1)
     return fail(SSM_ERR_INVALID, "batch, seqlen and dim must be >= 1");
   if (desc->batch > 65535) return fail(SSM_ERR_INVALID, "batch must be <= 65535");
+  // each extent bounded first, so that the products below cannot overflow
+  constexpr int64_t kMaxExtent = (int64_t(1) << 31) - 1;
+  if (desc->seqlen > kMaxExtent || desc->dim > kMaxExtent || desc->ld_x < 0 || desc->ld_x > kMaxExtent)
+    return fail(SSM_ERR_INVALID, "seqlen, dim and ld_x must be < 2^31");
   if (desc->seqlen * desc->dim > (int64_t(1) << 31) - 1) return fail(SSM_ERR_INVALID, "seqlen*dim must be < 2^31");
   if (desc->ksize < 1 || desc->ksize > kMaxK) return fail(SSM_ERR_INVALID, "ksize must be in 1..8");
   if (desc->dtype != SSM_F32 && desc->dtype != SSM_BF16) return fail(SSM_ERR_INVALID, "dtype must be SSM_F32 or SSM_BF16");

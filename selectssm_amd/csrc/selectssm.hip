@@ -1438,7 +1438,12 @@ int validate(const ssm_desc_t* desc, Shape* s) {
     return fail(SSM_ERR_INVALID, "batch, seqlen and dim must be >= 1");
   if (desc->dstate < 1 || desc->dstate > 32) return fail(SSM_ERR_INVALID, "dstate must be in 1..32");
   if (desc->batch > kMaxGridY) return fail(SSM_ERR_INVALID, "batch must be <= 65535");
-  // per-batch-row byte offsets are 32-bit inside the kernels
+  // per-batch-row byte offsets are 32-bit inside the kernels; each extent is
+  // bounded first so that the products below cannot overflow
+  constexpr int64_t kMaxExtent = int64_t(1) << 30;
+  if (desc->seqlen > kMaxExtent || desc->dim > kMaxExtent || desc->ld_y < 0 || desc->ld_y > kMaxExtent ||
+      desc->ld_z < 0 || desc->ld_z > kMaxExtent || desc->ld_bc < 0 || desc->ld_bc > kMaxExtent)
+    return fail(SSM_ERR_INVALID, "seqlen, dim, ld_y, ld_z and ld_bc must be <= 2^30 (ld_*: 0 or >= the row width)");
   if (desc->seqlen * desc->dim > (int64_t(1) << 30) || desc->seqlen * desc->dstate > (int64_t(1) << 30))
     return fail(SSM_ERR_INVALID, "seqlen*dim and seqlen*dstate must be <= 2^30");
   if ((desc->seqlen + kCK - 1) / kCK * desc->dstate * desc->dim > (int64_t(1) << 30))
