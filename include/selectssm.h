@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define SSM_ABI_VERSION 6
+#define SSM_ABI_VERSION 7
 
 /* error codes */
 #define SSM_OK 0
@@ -44,12 +44,24 @@ extern "C" {
 
 /* desc.flags */
 #define SSM_REVERSE 1u    /* SelectiveSSM(reverse=True): y written at L-1-t (selectssm.py:167-168, 230-231) */
-#define SSM_COMPLEMENT 2u /* with REVERSE: channel also mirrored, D-1-d (rcps.py:10-13) */
-#define SSM_SKIP 4u       /* y += u*Dskip with u in the scan domain (selectssm.py:238) */
+#define SSM_COMPLEMENT 2u /* channel mirrored, D-1-d: with REVERSE the RC map (rcps.py:10-13); alone, a
+                             channel-only map (the reference pairs it with REVERSE, selectssm.py:116) */
+#define SSM_SKIP 4u       /* y += u*Dskip with u in the scan domain (selectssm.py:238): the output
+                             position (p,q) adds u[p,q]*Dskip[q], u read at the output position itself
+                             (for a reverse scan the reference's quirk), unless SSM_SKIP_MAP */
 #define SSM_GATE 8u       /* y *= silu(z) (BidirectionalMamba, selectssm.py:335-336) */
 #define SSM_DELTA_SOFTPLUS 16u /* delta holds the pre-activation: the scan uses softplus(delta)
                                   (selectssm.py:210) and ssm_bwd's ddelta is the gradient with
                                   respect to that pre-activation */
+#define SSM_SKIP_MAP 32u        /* the skip's u is read at a map of the scan position instead of
+                                   at the output position: the output position of scan step (t,d)
+                                   adds u[S(t,d)]*Dskip[column of S(t,d)], S given by the two bits
+                                   below.  Conjugating a SelectiveSSM by a flip G (e.g. the RC map
+                                   of an RCPS wrapper, rcps.py:61-72) keeps the scan and moves the
+                                   output map to G o F and the skip source to F, F the module's own
+                                   flip (selectssm.py:167-168) */
+#define SSM_SKIP_REVERSE 64u    /* with SSM_SKIP_MAP: S reverses time, t -> L-1-t */
+#define SSM_SKIP_COMPLEMENT 128u /* with SSM_SKIP_MAP: S mirrors channels, d -> D-1-d */
 
 typedef struct ssm_desc {
   int64_t batch;          /* B */
@@ -203,7 +215,7 @@ typedef struct ssm_conv_desc {
   int64_t dim;            /* D */
   int32_t ksize;          /* K (shift_conv_size), 1..8 */
   int32_t dtype;          /* SSM_F32 or SSM_BF16 for x, u, du, dx; w and dw are f32 */
-  uint32_t flags;         /* SSM_REVERSE | SSM_COMPLEMENT */
+  uint32_t flags;         /* SSM_REVERSE (time) | SSM_COMPLEMENT (channel), either or both */
   int32_t activation;     /* SSM_ACT_* */
   int64_t ld_x;           /* elements between consecutive time rows of x; 0 = dim (x may be a
                              column slice of in_proj's output, selectssm.py:319); dx is always

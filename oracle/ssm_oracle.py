@@ -45,7 +45,11 @@ Pinning (what checks each function, in ``tests/test_oracle.py``):
                           torch's fp64 rms_norm / layer_norm
   gelu_tanh               gelu(x) - gelu(-x) = x, asymptotes, torch's fp64
                           tanh-approximate gelu
-  ssm_block_forward/_bwd  explicit np.flip composition; finite differences
+  ssm_block_forward/_bwd  explicit np.flip composition; finite differences;
+                          the general index maps (out_map, skip_map) reduce to the
+                          reference's defaults and are checked element by element
+                          on a brute-force loop; finite differences for all of them
+  flip_maps               the four flips against explicit index loops
 """
 from __future__ import annotations
 
@@ -203,8 +207,26 @@ def flip_domain(x, complement: bool):
     return np.flip(x, axis=(-2, -1) if complement else -2)
 
 
+def flip_maps(x, time_rev: bool, chan_rev: bool):
+    """x read through an index map reversing time and/or channels:
+    out[..., t, d] = x[..., L-1-t if time_rev else t, D-1-d if chan_rev else d].
+    ``flip_domain`` (selectssm.py:168) and the RC action (rcps.py:10-13) are two of
+    its four cases.  An involution."""
+    axes = tuple(ax for ax, on in ((-2, time_rev), (-1, chan_rev)) if on)
+    x = np.asarray(x, np.float64)
+    return np.flip(x, axis=axes) if axes else x
+
+
+def _block_maps(reverse, complement, out_map, skip_map):
+    """(output map, skip source map) as (time, channel) bits: by default the module's
+    flip (selectssm.py:167-168) and, for the skip, the output position itself
+    (selectssm.py:238 adds u at the output position: the reverse-mode quirk)."""
+    om = tuple(out_map) if out_map is not None else (bool(reverse), bool(reverse and complement))
+    return om, (om if skip_map is None else tuple(skip_map))
+
+
 def ssm_block_forward(u, delta, A, B, C, Dskip=None, z=None, reverse=False, complement=False,
-                      delta_softplus=False):
+                      delta_softplus=False, out_map=None, skip_map=None):
     """Scan + the scan-adjacent epilogue of ``SelectiveSSM``/``BidirectionalMamba``.
 
     u, delta, B, C are in the scan domain (already flipped when reverse=True,
@@ -215,26 +237,33 @@ def ssm_block_forward(u, delta, A, B, C, Dskip=None, z=None, reverse=False, comp
       y = y * silu(z)    BidirectionalMamba gate      (selectssm.py:335-336)
     delta_softplus: ``delta`` is the pre-activation, the scan uses softplus(delta)
     (selectssm.py:210).
+
+    General index maps (the conjugated modules of an RCPS stack): ``out_map``
+    (time, channel) places scan position (t, d) at O(t, d) of the output, and
+    ``skip_map`` S reads the skip's u at S(t, d) (D of its channel):
+      y_out[O(t,d)] = y_scan[t,d] + u[S(t,d)] * D[col S(t,d)],  then the gate.
+    The defaults reproduce the reference: O the module's flip, S = O.
     """
+    om, sm = _block_maps(reverse, complement, out_map, skip_map)
     if delta_softplus:
         delta = softplus(delta)
     y = scan_forward(u, delta, A, B, C)
-    if reverse:
-        y = flip_domain(y, complement)
     if Dskip is not None:
-        y = y + np.asarray(u, np.float64) * np.asarray(Dskip, np.float64)
+        y = y + flip_maps(np.asarray(u, np.float64) * np.asarray(Dskip, np.float64), *sm)
+    y = flip_maps(y, *om)
     if z is not None:
         y = y * silu(z)
     return y
 
 
 def ssm_block_backward(u, delta, A, B, C, dout, Dskip=None, z=None, reverse=False, complement=False,
-                       delta_softplus=False):
+                       delta_softplus=False, out_map=None, skip_map=None):
     """Chain rule through ``ssm_block_forward`` in fp64.
 
     Returns (du, ddelta, dA, dB, dC, dD, dz); dD / dz are None when unused.
     With delta_softplus, ddelta is w.r.t. the pre-activation (times sigmoid).
     """
+    om, sm = _block_maps(reverse, complement, out_map, skip_map)
     dsig = None
     if delta_softplus:
         dsig = sigmoid(delta)
@@ -244,24 +273,23 @@ def ssm_block_backward(u, delta, A, B, C, dout, Dskip=None, z=None, reverse=Fals
     dz = None
     if z is not None:
         pre = scan_forward(u, delta, A, B, C)
-        if reverse:
-            pre = flip_domain(pre, complement)
         if Dskip is not None:
-            pre = pre + u64 * np.asarray(Dskip, np.float64)
+            pre = pre + flip_maps(u64 * np.asarray(Dskip, np.float64), *sm)
+        pre = flip_maps(pre, *om)
         dz = dout * pre * silu_grad(z)
         dy = dout * silu(z)
     else:
         dy = dout
-    dD = None
-    du_skip = 0.0
-    if Dskip is not None:
-        dD = np.einsum("bld,bld->d", dy, u64)
-        du_skip = dy * np.asarray(Dskip, np.float64)
-    dys = flip_domain(dy, complement) if reverse else dy
+    dys = flip_maps(dy, *om)  # the gradient at the scan positions
     du, ddt, dA, dB, dC = scan_backward(u, delta, A, B, C, dys)
+    dD = None
+    if Dskip is not None:
+        ws = flip_maps(dys, *sm)  # the gradient reaching u[s] through the skip term read at s
+        dD = np.einsum("bld,bld->d", ws, u64)
+        du = du + ws * np.asarray(Dskip, np.float64)
     if dsig is not None:
         ddt = ddt * dsig
-    return du + du_skip, ddt, dA, dB, dC, dD, dz
+    return du, ddt, dA, dB, dC, dD, dz
 
 
 # --------------------------------------------------------------------------

@@ -26,12 +26,13 @@ def _act_code(activation):
 
 
 def _conv_desc(x, K, reverse, complement, activation):
+    """``reverse`` / ``complement``: time and channel reversal of x's index map, independently."""
     Bt, Ln, D = x.shape
     flags = 0
     if reverse:
         flags |= L.SSM_REVERSE
-        if complement:
-            flags |= L.SSM_COMPLEMENT
+    if complement:
+        flags |= L.SSM_COMPLEMENT
     ld = row_stride(x)
     if ld is None:
         raise ValueError("x must be contiguous or a column slice of a contiguous (B, L, W) tensor")
@@ -89,14 +90,22 @@ def conv1d_act(x, w, reverse=False, complement=False, activation="silu"):
     with x_s = x, or x flipped in time (and in channels with ``complement``) when
     ``reverse``.  ``activation``: "silu" (the reference's default), "relu" or None.
     """
+    if complement and not reverse:
+        complement = False  # the reference only looks at complement when reverse (selectssm.py:116, 167-168)
+    return conv1d_act_map(x, w, reverse, complement, activation)
+
+
+def conv1d_act_map(x, w, time_rev=False, chan_rev=False, activation="silu"):
+    """:func:`conv1d_act` with x read through any of the four flips of its (time,
+    channel) index map, independently: x_s[b,t,d] = x[b, L-1-t if time_rev else t,
+    D-1-d if chan_rev else d].  The module conjugations (an RCPS wrapper's RC map
+    composed with SelectiveSSM's own flip) need the channel-only map as well."""
     if x.dim() != 3:
         raise ValueError(f"x must be (B, L, D), got shape {tuple(x.shape)}")
     if not (x.is_cuda and w.is_cuda):
         raise ValueError("conv1d_act inputs must be GPU tensors (there is no CPU path)")
     if x.dtype not in _IO_DTYPES:
         raise TypeError(f"conv1d_act supports float32 and bfloat16 activations, got {x.dtype}")
-    if complement and not reverse:
-        complement = False  # the reference only looks at complement when reverse (selectssm.py:116, 167-168)
     _act_code(activation)
     w = _weight(w, x.shape[-1]).to(torch.float32).contiguous()
-    return ConvActFn.apply(as_rows(x, x.dtype)[0], w, bool(reverse), bool(complement), activation)
+    return ConvActFn.apply(as_rows(x, x.dtype)[0], w, bool(time_rev), bool(chan_rev), activation)

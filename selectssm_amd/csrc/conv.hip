@@ -251,8 +251,6 @@ int validate_conv(const ssm_conv_desc_t* desc, ConvShape* s) {
   if (desc->ksize < 1 || desc->ksize > kMaxK) return fail(SSM_ERR_INVALID, "ksize must be in 1..8");
   if (desc->dtype != SSM_F32 && desc->dtype != SSM_BF16) return fail(SSM_ERR_INVALID, "dtype must be SSM_F32 or SSM_BF16");
   if (desc->flags & ~(SSM_REVERSE | SSM_COMPLEMENT)) return fail(SSM_ERR_INVALID, "conv flags: only SSM_REVERSE, SSM_COMPLEMENT");
-  if ((desc->flags & SSM_COMPLEMENT) && !(desc->flags & SSM_REVERSE))
-    return fail(SSM_ERR_INVALID, "SSM_COMPLEMENT requires SSM_REVERSE (selectssm.py:116)");
   if (desc->activation != SSM_ACT_NONE && desc->activation != SSM_ACT_SILU && desc->activation != SSM_ACT_RELU)
     return fail(SSM_ERR_INVALID, "activation must be SSM_ACT_NONE, SSM_ACT_SILU or SSM_ACT_RELU");
   s->B = (int)desc->batch;

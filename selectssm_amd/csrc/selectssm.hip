@@ -205,21 +205,28 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
   const int d = cb * kBlkCh + cw;
   const bool valid = d < D;
   const int dc = valid ? d : 0;
+  // output map: time (rev) and channel (comp) reversal of the scan position
   const bool rev = p.flags & SSM_REVERSE;
-  const bool comp = rev && (p.flags & SSM_COMPLEMENT);
-  // the skip of a forward scan uses the staged u itself; the reverse skip and
-  // the gate need the extra staging of EPI builds
+  const bool comp = (p.flags & SSM_COMPLEMENT) != 0;
+  // skip source map: the skip adds u at this map of the scan position (and D of
+  // its channel); by default the output position itself, the reference's quirk
+  const bool smap = (p.flags & SSM_SKIP_MAP) != 0;
+  const bool srev = smap ? (p.flags & SSM_SKIP_REVERSE) != 0 : rev;
+  const bool scomp = smap ? (p.flags & SSM_SKIP_COMPLEMENT) != 0 : comp;
+  // the skip from the scan position uses the staged u itself; any other skip
+  // source and the gate need the extra staging of EPI builds
   const bool skip = (p.flags & SSM_SKIP) != 0;
   const bool gate = EPI && (p.flags & SSM_GATE);
-  const bool stage_eu = EPI && skip && rev;  // u at the output position is another element
-  const int q = comp ? D - 1 - dc : dc;      // output channel of this lane
-  const float Dq = (skip && valid) ? p.Dskip[q] : 0.0f;
+  const bool stage_eu = EPI && skip && (srev || scomp);  // the skip's u is another element
+  const int q = comp ? D - 1 - dc : dc;                  // output channel of this lane
+  const float Dq = (skip && valid) ? p.Dskip[scomp ? D - 1 - dc : dc] : 0.0f;
   const int scol = tid & (kBlkCh - 1);
   const int srow0 = wave;  // = tid / kBlkCh: the staged rows of a wave are uniform
   const int sd = cb * kBlkCh + scol;
   const bool svalid = sd < D;
   const int sdc = svalid ? sd : 0;
-  const int sq = comp ? D - 1 - sdc : sdc;  // output channel of the staged column
+  const int sq = comp ? D - 1 - sdc : sdc;     // output channel of the staged column (z)
+  const int sqs = scomp ? D - 1 - sdc : sdc;   // skip-source channel of the staged column (u)
   const bool full_cb = (cb + 1) * kBlkCh <= D;
 
   float A2[SPL], h[SPL];
@@ -266,6 +273,7 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
   const buf_t ru = make_buf(u_b), rdt = make_buf(dt_b), rB = make_buf(B_b), rC = make_buf(C_b);
   const buf_t rz = make_buf(EPI ? z_b : u_b), ry = make_buf(y_b), rck = make_buf(ck_b != nullptr ? ck_b : p.A);
   const uint32_t cb_c = (uint32_t)(sdc * sizeof(T)), cb_q = (uint32_t)(sq * sizeof(T));
+  const uint32_t cb_qs = (uint32_t)(sqs * sizeof(T));
   const uint32_t cb_dt = (uint32_t)(scol_dt * sizeof(T));
 
   // fetch() only issues loads (clamped addresses, raw values); commit(), run
@@ -311,8 +319,9 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
 #pragma unroll
       for (int k = 0; k < RPT; ++k) {
         const int tc = min(t0 + srow0 + k * RSTEP, L - 1);
-        const int pr = rev ? L - 1 - tc : tc;
-        if (stage_eu) r_eu[k] = bldr<T>(ru, cb_q, (uint32_t)pr * rowb);
+        const int pr = rev ? L - 1 - tc : tc;    // output row (z)
+        const int prs = srev ? L - 1 - tc : tc;  // skip-source row (u)
+        if (stage_eu) r_eu[k] = bldr<T>(ru, cb_qs, (uint32_t)prs * rowb);
         if (gate) r_ez[k] = bldr<T>(rz, cb_q, (uint32_t)(pr * ldz * sizeof(T)));
       }
     }
@@ -735,22 +744,32 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
   int nj[SPL];  // state of slot j
 #pragma unroll
   for (int j = 0; j < SPL; ++j) nj[j] = SPL * g + (j ^ sig);
+  // output map (rev, comp) and skip source map (srev, scomp), as in the forward
   const bool rev = p.flags & SSM_REVERSE;
-  const bool comp = rev && (p.flags & SSM_COMPLEMENT);
+  const bool comp = (p.flags & SSM_COMPLEMENT) != 0;
+  const bool smap = (p.flags & SSM_SKIP_MAP) != 0;
+  const bool srev = smap ? (p.flags & SSM_SKIP_REVERSE) != 0 : rev;
+  const bool scomp = smap ? (p.flags & SSM_SKIP_COMPLEMENT) != 0 : comp;
   const bool gate = EPI && (p.flags & SSM_GATE);
-  const bool skip = (p.flags & SSM_SKIP) != 0;  // non-EPI builds run only the forward-scan skip
-  const bool stage_dyo = EPI && skip && rev;    // gated dy at the unmirrored (t,d) for the skip term
-  const bool stage_eu = gate && skip && rev;    // u at the output position for y_pre
+  const bool skip = (p.flags & SSM_SKIP) != 0;  // non-EPI builds run only the skip from the scan position
+  // u[t,d] is added (times D[d]) at the output position O(S(t,d)) with S the
+  // skip source map: its gradient reads the gated dy there, which is the lane's
+  // own staged dy when S is the identity and another element otherwise
+  const bool stage_dyo = EPI && skip && (srev || scomp);
+  const bool stage_eu = gate && skip && (srev || scomp);  // the skip's u inside y_pre for dz
+  const bool mrev = rev != srev, mcomp = comp != scomp;   // O(S(t,d)) relative to (t,d)
   const bool dsp = p.flags & SSM_DELTA_SOFTPLUS;
   const int q = comp ? D - 1 - dc : dc;
-  const float Dd = (skip && valid) ? p.Dskip[dc] : 0.0f;  // y_out[t,d] holds u[t,d] D[d] (selectssm.py:238)
-  const float Dq = (skip && valid) ? p.Dskip[q] : 0.0f;   // the skip inside y_pre at the output position
+  const float Dd = (skip && valid) ? p.Dskip[dc] : 0.0f;  // u[t,d] carries D[d] (selectssm.py:238)
+  const float Dq = (skip && valid) ? p.Dskip[scomp ? D - 1 - dc : dc] : 0.0f;  // the skip inside y_pre
   const int scol = tid & (kBlkCh - 1);
   const int srow0 = wave;  // = tid / kBlkCh: the staged rows of a wave are uniform
   const int sd = cb * kBlkCh + scol;
   const bool svalid = sd < D;
   const int sdc = svalid ? sd : 0;
-  const int sq = comp ? D - 1 - sdc : sdc;
+  const int sq = comp ? D - 1 - sdc : sdc;     // output channel of the staged column
+  const int sqs = scomp ? D - 1 - sdc : sdc;   // skip-source channel
+  const int sqm = mcomp ? D - 1 - sdc : sdc;   // channel of O(S(.)) for the skip's gradient
   const bool full_cb = (cb + 1) * kBlkCh <= D;
   // after the exchange over state groups, row g >> 1 of the wave holds
   // du (rows 0, 1) or ddelta (rows 2, 3) of one of 2 steps, twice (both halves)
@@ -865,12 +884,14 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
 #pragma unroll
       for (int k = 0; k < RPT; ++k) {
         const int tc = min(t0 + srow0 + k * RSTEP, L - 1);
-        const int pr = rev ? L - 1 - tc : tc;
+        const int pr = rev ? L - 1 - tc : tc;     // output row
+        const int prs = srev ? L - 1 - tc : tc;   // skip-source row
+        const int prm = mrev ? L - 1 - tc : tc;   // row of O(S(.))
         if (gate) r_gz[k] = ld32r(z_b, (uint32_t)(pr * ldz + sq));
-        if (stage_eu) r_eu[k] = ld32r(u_b, (uint32_t)(pr * D + sq));
+        if (stage_eu) r_eu[k] = ld32r(u_b, (uint32_t)(prs * D + sqs));
         if (stage_dyo) {
-          r_dyo[k] = ld32r(dy_b, (uint32_t)(tc * ldy + sdc));
-          if (gate) r_zo[k] = ld32r(z_b, (uint32_t)(tc * ldz + sdc));
+          r_dyo[k] = ld32r(dy_b, (uint32_t)(prm * ldy + sqm));
+          if (gate) r_zo[k] = ld32r(z_b, (uint32_t)(prm * ldz + sqm));
         }
       }
     }
@@ -1218,7 +1239,7 @@ __device__ __forceinline__ void bwd_agg_body(const BwdArgs<T>& p, const int b) {
   const bool valid = d < D;
   const int dc = valid ? d : 0;
   const bool rev = p.flags & SSM_REVERSE;
-  const bool comp = rev && (p.flags & SSM_COMPLEMENT);
+  const bool comp = (p.flags & SSM_COMPLEMENT) != 0;
   const bool gate = EPI && (p.flags & SSM_GATE);
   const bool dsp = p.flags & SSM_DELTA_SOFTPLUS;
   const int scol = tid & (kBlkCh - 1);
@@ -1449,10 +1470,11 @@ int validate(const ssm_desc_t* desc, Shape* s) {
   if ((desc->seqlen + kCK - 1) / kCK * desc->dstate * desc->dim > (int64_t(1) << 30))
     return fail(SSM_ERR_INVALID, "checkpoints of one batch row must hold <= 2^30 floats");
   if (desc->dtype != SSM_F32 && desc->dtype != SSM_BF16) return fail(SSM_ERR_INVALID, "dtype must be SSM_F32 or SSM_BF16");
-  if (desc->flags & ~(SSM_REVERSE | SSM_COMPLEMENT | SSM_SKIP | SSM_GATE | SSM_DELTA_SOFTPLUS))
+  if (desc->flags & ~(SSM_REVERSE | SSM_COMPLEMENT | SSM_SKIP | SSM_GATE | SSM_DELTA_SOFTPLUS | SSM_SKIP_MAP |
+                      SSM_SKIP_REVERSE | SSM_SKIP_COMPLEMENT))
     return fail(SSM_ERR_INVALID, "unknown flag bits");
-  if ((desc->flags & SSM_COMPLEMENT) && !(desc->flags & SSM_REVERSE))
-    return fail(SSM_ERR_INVALID, "SSM_COMPLEMENT requires SSM_REVERSE (selectssm.py:116)");
+  if ((desc->flags & (SSM_SKIP_REVERSE | SSM_SKIP_COMPLEMENT)) && !(desc->flags & SSM_SKIP_MAP))
+    return fail(SSM_ERR_INVALID, "SSM_SKIP_REVERSE / SSM_SKIP_COMPLEMENT need SSM_SKIP_MAP");
   if (desc->delta_broadcast != 0 && desc->delta_broadcast != 1)
     return fail(SSM_ERR_INVALID, "delta_broadcast must be 0 or 1");
   if (desc->segments < 0 || desc->segments > kMaxSeg) return fail(SSM_ERR_INVALID, "segments must be in 0..1024");
@@ -1472,8 +1494,12 @@ int validate(const ssm_desc_t* desc, Shape* s) {
   s->ldz = desc->ld_z ? (int)desc->ld_z : s->D;
   s->ldbc = desc->ld_bc ? (int)desc->ld_bc : s->N;
   s->nblk = (s->L + kCK - 1) / kCK;
-  // extra epilogue staging: the gate, and the reverse skip's u at the mirrored position
-  s->epi = (desc->flags & SSM_GATE) || ((desc->flags & SSM_SKIP) && (desc->flags & SSM_REVERSE));
+  // extra epilogue staging: the gate, and a skip whose u is not at the scan position
+  // (by default the skip source is the output position: the reverse skip's quirk)
+  const uint32_t f = desc->flags;
+  const bool skip_moved = (f & SSM_SKIP_MAP) ? (f & (SSM_SKIP_REVERSE | SSM_SKIP_COMPLEMENT)) != 0
+                                             : (f & (SSM_REVERSE | SSM_COMPLEMENT)) != 0;
+  s->epi = (f & SSM_GATE) || ((f & SSM_SKIP) && skip_moved);
   s->spl_f = s->N <= 16 ? 4 : 8;  // 4 state rows per forward wave
   s->spl_b = s->N <= 16 ? 2 : 4;  // 8 state groups per backward wave
   choose_segments(desc, s);

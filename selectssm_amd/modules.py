@@ -31,7 +31,7 @@ from typing import Optional, Union
 import torch
 import torch.nn.functional as F
 
-from .conv import conv1d_act
+from .conv import conv1d_act, conv1d_act_map
 from .scan import (_check_recursion, as_rows, bidirectional_selective_scan, needs_grad, resolve_chunking, scan_bwd,
                    scan_bwd_pair, scan_fwd, scan_fwd_pair, selective_scan)
 
@@ -81,10 +81,20 @@ class Dense(torch.nn.Module):
         else:
             self.register_parameter("bias", None)
 
-    def forward(self, x):
+    def forward(self, x, flip_in: bool = False, flip_out: bool = False):
+        """x @ kernel + bias.  ``flip_in`` / ``flip_out`` reverse the kernel's input rows /
+        output columns (and the bias): the layer conjugated by a channel flip of its
+        input / output, as an RC-conjugated block needs (parameters are permuted, the
+        activations are not)."""
         w = self.kernel.to(x.dtype)
+        b = None if self.bias is None else self.bias.to(x.dtype)
+        if flip_in:
+            w = w.flip(0)
+        if flip_out:
+            w = w.flip(1)
+            b = None if b is None else b.flip(0)
         x2 = x.reshape(-1, x.shape[-1])
-        y = _DenseFn.apply(x2, w, None if self.bias is None else self.bias.to(x.dtype))
+        y = _DenseFn.apply(x2, w, b)
         return y.reshape(*x.shape[:-1], w.shape[1])
 
 
@@ -195,12 +205,14 @@ def _core_project(u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, N, rank):
     return A, dt_low, dt.contiguous(), Bc, Cc
 
 
-def _core_forward(u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, Dp, z, N, rank, reverse, complement, want_ckpt, y_out=None):
+def _core_forward(u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, Dp, z, N, rank, reverse, complement, want_ckpt, y_out=None,
+                  skip_map=None):
     """Projections + scan (selectssm.py:190-238); returns (y, saved tensors).  The scan
-    writes its checkpoints only when ``want_ckpt`` (a backward will run)."""
+    writes its checkpoints only when ``want_ckpt`` (a backward will run).  ``reverse``,
+    ``complement``: the output map; ``skip_map``: the skip's source map (scan_fwd)."""
     A, dt_low, dt, Bc, Cc = _core_project(u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, N, rank)
     y, ckpt = scan_fwd(u, dt, A, Bc, Cc, Dp, z, reverse, complement, want_ckpt=want_ckpt, delta_softplus=True,
-                       y_out=y_out)
+                       y_out=y_out, skip_map=skip_map)
     return y, (u, A, Wbc, Wdt, Wp, Dp, z, dt_low, dt, Bc, Cc, ckpt)
 
 
@@ -210,18 +222,19 @@ def _dbc_buffer(u, N):
     return torch.empty(*u.shape[:-1], 2 * N, dtype=u.dtype, device=u.device)
 
 
-def _scan_call(saved, reverse, complement, N):
+def _scan_call(saved, reverse, complement, N, skip_map=None):
     """The scan's arguments for the scan_*_pair launchers, from _core_forward's saved tensors."""
     u, A, _, _, _, Dp, z, _, dt, Bc, Cc, ckpt = saved
     return dict(u=u, delta=dt, A=A, B=Bc, C=Cc, Dskip=Dp, z=z, reverse=reverse, complement=complement,
-                delta_softplus=True, dbc_out=_dbc_buffer(u, N))
+                delta_softplus=True, dbc_out=_dbc_buffer(u, N), skip_map=skip_map)
 
 
-def _core_backward(saved, dy, N, rank, reverse, complement):
+def _core_backward(saved, dy, N, rank, reverse, complement, skip_map=None):
     """Gradients of _core_forward for (u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, D, z)."""
     u, A, Wbc, Wdt, Wp, Dp, z, dt_low, dt, Bc, Cc, ckpt = saved
     dbc = _dbc_buffer(u, N)
-    grads = scan_bwd(u, dt, A, Bc, Cc, Dp, z, ckpt, dy, reverse, complement, delta_softplus=True, dbc_out=dbc)
+    grads = scan_bwd(u, dt, A, Bc, Cc, Dp, z, ckpt, dy, reverse, complement, delta_softplus=True, dbc_out=dbc,
+                     skip_map=skip_map)
     return _core_param_grads(saved, grads, dbc, N, rank)
 
 
@@ -285,53 +298,71 @@ class _SSMCoreFn(torch.autograd.Function):
     beta = 1) instead of separate addition kernels."""
 
     @staticmethod
-    def forward(ctx, u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, Dp, z, N, rank, reverse, complement, want_ckpt):
-        y, saved = _core_forward(u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, Dp, z, N, rank, reverse, complement, want_ckpt)
+    def forward(ctx, u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, Dp, z, N, rank, reverse, complement, skip_map, want_ckpt):
+        y, saved = _core_forward(u, A_log, Wbc, bbc, Wdt, bdt, Wp, bp, Dp, z, N, rank, reverse, complement, want_ckpt,
+                                 skip_map=skip_map)
         ctx.save_for_backward(*saved)
-        ctx.cfg = (N, rank, reverse, complement)
+        ctx.cfg = (N, rank, reverse, complement, skip_map)
         return y
 
     @staticmethod
     def backward(ctx, dy):
         dy, _ = as_rows(dy, ctx.saved_tensors[0].dtype)
-        return (*_core_backward(ctx.saved_tensors, dy, *ctx.cfg), None, None, None, None, None)
+        return (*_core_backward(ctx.saved_tensors, dy, *ctx.cfg), None, None, None, None, None, None)
 
 
 class _PairCoreFn(torch.autograd.Function):
     """Both BidirectionalMamba directions' cores (_SSMCoreFn), each writing its y
-    straight into its half of the concatenated output (selectssm.py:325-336)."""
+    straight into its half of the concatenated output (selectssm.py:325-336).
+    ``maps``: per direction, the scan's output map (time, channel) and skip map
+    (SelectiveSSM._maps)."""
 
     @staticmethod
     def forward(ctx, uf, A_logf, Wbcf, bbcf, Wdtf, bdtf, Wpf, bpf, Df, zf,
-                ur, A_logr, Wbcr, bbcr, Wdtr, bdtr, Wpr, bpr, Dr, zr, N, rank, complement, want_ckpt):
+                ur, A_logr, Wbcr, bbcr, Wdtr, bdtr, Wpr, bpr, Dr, zr, N, rank, maps, want_ckpt):
         B_, L_, E = uf.shape
         y = torch.empty(B_, L_, 2 * E, dtype=uf.dtype, device=uf.device)
         pf = _core_project(uf, A_logf, Wbcf, bbcf, Wdtf, bdtf, Wpf, bpf, N, rank)
         pr = _core_project(ur, A_logr, Wbcr, bbcr, Wdtr, bdtr, Wpr, bpr, N, rank)
-        # both directions' scans in one pair call (their time-split aggregate passes share a launch)
-        calls = [dict(u=u, delta=p[2], A=p[0], B=p[3], C=p[4], Dskip=Dp, z=z, reverse=rev, complement=comp,
-                      delta_softplus=True, y_out=yo, want_ckpt=want_ckpt)
-                 for u, p, Dp, z, rev, comp, yo in ((uf, pf, Df, zf, False, False, y[..., :E]),
-                                                    (ur, pr, Dr, zr, True, complement, y[..., E:]))]
+        # both directions' scans in one pair call (one launch per kernel for the two)
+        calls = [dict(u=u, delta=p[2], A=p[0], B=p[3], C=p[4], Dskip=Dp, z=z, reverse=om[0], complement=om[1],
+                      skip_map=sm, delta_softplus=True, y_out=yo, want_ckpt=want_ckpt)
+                 for u, p, Dp, z, (om, sm), yo in ((uf, pf, Df, zf, maps[0], y[..., :E]),
+                                                   (ur, pr, Dr, zr, maps[1], y[..., E:]))]
         (_, ckf), (_, ckr) = scan_fwd_pair(calls)
         sf = (uf, pf[0], Wbcf, Wdtf, Wpf, Df, zf, pf[1], pf[2], pf[3], pf[4], ckf)
         sr = (ur, pr[0], Wbcr, Wdtr, Wpr, Dr, zr, pr[1], pr[2], pr[3], pr[4], ckr)
         ctx.save_for_backward(*sf, *sr)
-        ctx.cfg = (N, rank, complement, len(sf))
+        ctx.cfg = (N, rank, maps, len(sf))
         return y
 
     @staticmethod
     def backward(ctx, dy):
-        N, rank, complement, k = ctx.cfg
+        N, rank, maps, k = ctx.cfg
         saved = ctx.saved_tensors
         E = saved[0].shape[-1]
         dy, _ = as_rows(dy, saved[0].dtype)
         sf, sr = saved[:k], saved[k:]
-        cf, cr = _scan_call(sf, False, False, N), _scan_call(sr, True, complement, N)
+        (omf, smf), (omr, smr) = maps
+        cf, cr = _scan_call(sf, omf[0], omf[1], N, smf), _scan_call(sr, omr[0], omr[1], N, smr)
         scan_gf, scan_gr = scan_bwd_pair([dict(cf, ckpt=sf[-1], dy=dy[..., :E]), dict(cr, ckpt=sr[-1], dy=dy[..., E:])])
         gf = _core_param_grads(sf, scan_gf, cf["dbc_out"], N, rank)
         gr = _core_param_grads(sr, scan_gr, cr["dbc_out"], N, rank)
         return (*gf, *gr, None, None, None, None)
+
+
+def _xor(a, b):
+    """Composition of two flips given as (time, channel) reversal bits (they commute)."""
+    return (bool(a[0]) != bool(b[0]), bool(a[1]) != bool(b[1]))
+
+
+RC_MAP = (True, True)  # RC(x)[b,l,d] = x[b,L-1-l,D-1-d] (rcps.py:10-13, 37-39)
+TIME_MAP = (True, False)
+
+
+def rc_flip(x: torch.Tensor) -> torch.Tensor:
+    """The RC action on an activation, as a materialised flip (modules without index maps)."""
+    return torch.flip(x, dims=(-2, -1))
 
 
 class SelectiveSSM(_FlaxModule):
@@ -399,10 +430,29 @@ class SelectiveSSM(_FlaxModule):
         d = self.diagnostics
         return bool(d) and any(k in d for k in ("ssm_coeffs", "ssm_residual", "ssm_output_norm"))
 
-    def _prepare(self, x: torch.Tensor, projections: bool = True) -> dict:
+    def _flip(self):
+        """The module's own flip of x (selectssm.py:167-168) as (time, channel) bits."""
+        return (bool(self.reverse), bool(self.reverse and self.complement))
+
+    def _maps(self, conj=None):
+        """(conv map, scan output map, skip map) of the fused path.  Without ``conj``
+        the conv reads x through the module's flip F, the scan writes y through F and
+        the skip adds u at the output position (skip map None, the reference's
+        convention).  Conjugated by a flip G, x -> G(M(G(x))), the conv reads through
+        G o F, y is written through G o F and the skip's u is read at F of the scan
+        position: the scan itself and every projection are unchanged, only the
+        index maps move."""
+        F = self._flip()
+        if conj is None:
+            return F, F, None
+        GF = _xor(conj, F)
+        return GF, GF, F
+
+    def _prepare(self, x: torch.Tensor, projections: bool = True, conv_map=None) -> dict:
         """Everything of __call__ before the scan (selectssm.py:156-228): the scan's
         operands in the scan domain, with delta before its softplus (only the conv
-        output u when ``projections`` is False)."""
+        output u when ``projections`` is False).  ``conv_map``: the conv's (time,
+        channel) index map when not the module's own flip (a conjugation)."""
         if self.features is None:
             self._build(x.shape[-1], x.device)
         B, L, D = x.shape
@@ -421,8 +471,8 @@ class SelectiveSSM(_FlaxModule):
             raise Exception(f"Unknown activation: {self.activation}")
         coeffs = bool(diag) and "ssm_coeffs" in diag
         fused = self.activation in _FUSED_CONV_ACTS and not coeffs
-        u = conv1d_act(x, self.shift_conv.kernel, self.reverse, self.complement,
-                       self.activation if fused else None)
+        cmap = self._flip() if conv_map is None else conv_map
+        u = conv1d_act_map(x, self.shift_conv.kernel, cmap[0], cmap[1], self.activation if fused else None)
         if coeffs:
             self._sow("diagnostics", "conv_mean", u.mean())
             self._sow("diagnostics", "conv_sd", u.std(unbiased=False))
@@ -516,12 +566,44 @@ class SelectiveSSM(_FlaxModule):
                 self.dt_proj.kernel if self.dt_proj_enabled else None,
                 self.dt_proj.bias if self.dt_proj_enabled else None, self.D, z)
 
-    def _core(self, u: torch.Tensor, z: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """Projections + scan from the conv output u in one autograd node (see _SSMCoreFn)."""
+    def _core(self, u: torch.Tensor, z: Optional[torch.Tensor] = None, conj=None) -> torch.Tensor:
+        """Projections + scan from the conv output u in one autograd node (see _SSMCoreFn),
+        with the output and skip maps of :meth:`_maps`."""
         zz = None if z is None else as_rows(z, u.dtype)[0]
         args = self._core_args(u, zz)
-        return _SSMCoreFn.apply(*args, self.hidden_features, self.rank, self.reverse, self.complement,
-                                needs_grad(*args))
+        _, om, sm = self._maps(conj)
+        return _SSMCoreFn.apply(*args, self.hidden_features, self.rank, om[0], om[1], sm, needs_grad(*args))
+
+    def _conj_fusable(self, gate_activation="silu") -> bool:
+        """Whether a conjugated call runs on index maps alone (the fused path: no
+        diagnostics that need intermediates, a fused conv activation and gate)."""
+        return (not self._needs_intermediates() and self.activation in _FUSED_CONV_ACTS
+                and gate_activation == "silu")
+
+    def forward_conj(self, x: torch.Tensor, conj, train: bool = False, gate: Optional[torch.Tensor] = None,
+                     gate_activation: str = "silu") -> torch.Tensor:
+        """G(self(G(x))) for a flip G = ``conj`` ((time, channel) reversal bits), with
+        ``gate`` applied at the output positions: G(self(G(x)) * act(G(gate)))
+        = G(self(G(x))) * act(gate).  No activation is flipped: the conv reads x
+        through G o F, the scan writes through G o F and takes the skip's u at F of
+        the scan position (:meth:`_maps`).  Falls back to materialised flips where
+        the fused path does not apply."""
+        if not self._conj_fusable(gate_activation if gate is not None else "silu"):
+            flip = lambda t: torch.flip(t, dims=[d for d, on in ((-2, conj[0]), (-1, conj[1])) if on])
+            g = None if gate is None else flip(gate)
+            return flip(self.forward(flip(x), train, gate=g, gate_activation=gate_activation))
+        if self.features is None:
+            self._build(x.shape[-1], x.device)
+        cmap, _, _ = self._maps(conj)
+        u = self._prepare(x, projections=False, conv_map=cmap)["u"]
+        y = self._core(u, gate, conj)
+        self._finish(None)
+        return y
+
+    def forward_rc(self, x: torch.Tensor, train: bool = False) -> torch.Tensor:
+        """RC(self(RC(x))): this module as the inner module of an RCPSWrapper's
+        antisense half (rcps.py:61-72), on index maps (:meth:`forward_conj`)."""
+        return self.forward_conj(x, RC_MAP, train)
 
 
 class RMSNorm(torch.nn.Module):
@@ -532,10 +614,16 @@ class RMSNorm(torch.nn.Module):
         self.eps = eps
         self.scale = torch.nn.Parameter(torch.ones(D, device=device))
 
-    def forward(self, x):
+    def forward(self, x, flip: bool = False):
+        """``flip``: the per-channel scale reversed (the norm conjugated by a channel flip)."""
         # x * rsqrt(mean(x^2) + eps) * scale over the last axis, as one op
-        y = F.rms_norm(x.float(), (x.shape[-1],), self.scale, self.eps)
+        y = F.rms_norm(x.float(), (x.shape[-1],), self.scale.flip(0) if flip else self.scale, self.eps)
         return y.to(x.dtype)
+
+
+def _norm_forward_rc(self, x):
+    """RC(norm(RC(x))) = the norm with its per-channel parameters reversed."""
+    return self.forward(x, flip=True)
 
 
 class LayerNorm(torch.nn.Module):
@@ -547,8 +635,9 @@ class LayerNorm(torch.nn.Module):
         self.scale = torch.nn.Parameter(torch.ones(D, device=device))
         self.bias = torch.nn.Parameter(torch.zeros(D, device=device))
 
-    def forward(self, x):
-        return F.layer_norm(x.float(), (x.shape[-1],), self.scale, self.bias, self.eps).to(x.dtype)
+    def forward(self, x, flip: bool = False):
+        s, b = (self.scale.flip(0), self.bias.flip(0)) if flip else (self.scale, self.bias)
+        return F.layer_norm(x.float(), (x.shape[-1],), s, b, self.eps).to(x.dtype)
 
 
 class GroupNorm(torch.nn.Module):
@@ -562,14 +651,22 @@ class GroupNorm(torch.nn.Module):
         self.scale = torch.nn.Parameter(torch.ones(D, device=device))
         self.bias = torch.nn.Parameter(torch.zeros(D, device=device))
 
-    def forward(self, x):
+    def forward(self, x, flip: bool = False):
+        """``flip``: scale and bias reversed.  A channel flip maps group g onto group
+        groups-1-g with the same statistics, so that is the whole conjugation."""
         B, L, D = x.shape
         xf = x.float().reshape(B, L, self.groups, D // self.groups)
         # statistics over every non-batch axis within a group (time and the group's features)
         mean = xf.mean(dim=(1, 3), keepdim=True)
         var = xf.var(dim=(1, 3), keepdim=True, unbiased=False)
-        y = ((xf - mean) * torch.rsqrt(var + self.eps)).reshape(B, L, D) * self.scale + self.bias
+        s, b = (self.scale.flip(0), self.bias.flip(0)) if flip else (self.scale, self.bias)
+        y = ((xf - mean) * torch.rsqrt(var + self.eps)).reshape(B, L, D) * s + b
         return y.to(x.dtype)
+
+
+RMSNorm.forward_rc = _norm_forward_rc
+LayerNorm.forward_rc = _norm_forward_rc
+GroupNorm.forward_rc = _norm_forward_rc
 
 
 class BatchNorm(torch.nn.Module):
@@ -657,6 +754,27 @@ class BidirectionalMamba(_FlaxModule):
             self.mlp_proj = Dense(self.dense_expansion * D, D, device=device, generator=g)
 
     def forward(self, x: torch.Tensor, train: bool = False) -> torch.Tensor:
+        return self._run(x, train, rc=False)
+
+    def forward_rc(self, x: torch.Tensor, train: bool = False) -> torch.Tensor:
+        """RC(self(RC(x))): this block as the inner module of an RCPSWrapper's antisense
+        half (rcps.py:61-72), without flipping any activation.  With x' = RC(x):
+          * norm(x') = RC(norm~(x)), norm~ with its per-channel parameters reversed;
+          * in_proj(RC(n)) = T(n @ W~ + b), W~ = in_proj's kernel with its input rows
+            reversed, T the time reversal: every in_proj column block arrives
+            time-reversed and in its own channel order;
+          * each SSM therefore runs conjugated by T (SelectiveSSM._maps), its gate at
+            its output positions;
+          * RC(concat(..) @ W_out + b_out) = T(concat(..)) @ W^ + b^ with W^, b^ the
+            output columns (and bias) reversed; the residual RC(x') = x; the MLP
+            conjugates the same way (input rows, then output columns).
+        Only parameters are permuted.  BatchNorm (running statistics) and the unfused
+        diagnostics paths fall back to materialised flips."""
+        if self.norm_type == "batch" or self.diagnostics:
+            return rc_flip(self._run(rc_flip(x), train, rc=False))
+        return self._run(x, train, rc=True)
+
+    def _run(self, x: torch.Tensor, train: bool, rc: bool) -> torch.Tensor:
         if self.features is None:
             self._build(x.shape[-1], x.device)
         activate = _activation_fn(self.activation)
@@ -664,14 +782,15 @@ class BidirectionalMamba(_FlaxModule):
         if self.norm_type == "batch":
             x = self.BatchNorm_0(x, train)
         elif self.norm_type == "layer":
-            x = self.LayerNorm_0(x)
+            x = self.LayerNorm_0(x, flip=rc)
         elif self.norm_type == "group":
-            x = self.GroupNorm_0(x)
+            x = self.GroupNorm_0(x, flip=rc)
         elif self.norm_type == "rms":
-            x = self.RMSNorm_0(x)
+            x = self.RMSNorm_0(x, flip=rc)
         ED = self.ED
         n_in = 1 if self.tie_in_proj else 2
-        h = self.in_proj(x)
+        h = self.in_proj(x, flip_in=rc)
+        conj = TIME_MAP if rc else None
         # jnp.split at [ED, n_in*ED, (n_in+1)*ED] (selectssm.py:319-321)
         n_gate = 1 if self.tie_gate else 2
         blocks = _SplitCols.apply(h, *([ED] * (n_in + n_gate)))
@@ -684,31 +803,37 @@ class BidirectionalMamba(_FlaxModule):
                 and not self.ssm_rev._unfused_outputs()):
             f, r = self.ssm_fwd, self.ssm_rev
             if f._needs_intermediates() or r._needs_intermediates():
+                assert not rc  # forward_rc takes the materialised flips for diagnostics
                 pf = f._prepare(xf)
                 pr = r._prepare(xr)
                 pf["z"], pr["z"] = zf, zr
                 # both directions straight into the concatenated output (selectssm.py:335)
                 x = bidirectional_selective_scan(pf, pr, complement=self.complement, delta_softplus=True)
             else:
-                uf = f._prepare(xf, projections=False)["u"]
-                ur = r._prepare(xr, projections=False)["u"]
+                mf, mr = f._maps(conj), r._maps(conj)
+                uf = f._prepare(xf, projections=False, conv_map=mf[0])["u"]
+                ur = r._prepare(xr, projections=False, conv_map=mr[0])["u"]
                 io = uf.dtype
                 args = (*f._core_args(uf, as_rows(zf, io)[0]), *r._core_args(ur, as_rows(zr, io)[0]))
-                x = _PairCoreFn.apply(*args, f.hidden_features, f.rank, self.complement, needs_grad(*args))
+                x = _PairCoreFn.apply(*args, f.hidden_features, f.rank, (mf[1:], mr[1:]), needs_grad(*args))
             f._finish(None)
             r._finish(None)
+        elif rc:
+            yf = self.ssm_fwd.forward_conj(xf, TIME_MAP, train, gate=zf, gate_activation=self.activation)
+            yr = self.ssm_rev.forward_conj(xr, TIME_MAP, train, gate=zr, gate_activation=self.activation)
+            x = torch.cat([yf, yr], dim=-1) if self.concatenate_fwd_rev else yf + yr
         else:
             yf = self.ssm_fwd(xf, train, gate=zf, gate_activation=self.activation)
             yr = self.ssm_rev(xr, train, gate=zr, gate_activation=self.activation)
             x = torch.cat([yf, yr], dim=-1) if self.concatenate_fwd_rev else yf + yr
-        x = self.out_proj(x)
+        x = self.out_proj(x, flip_out=rc)
         x = skip + x
         if self.mlp_layer:
             skip = x
-            x = self.mlp(x)
+            x = self.mlp(x, flip_in=rc)
             x = F.dropout(x, self.mlp_dropout_rate, training=train)
             x = activate(x)
-            x = self.mlp_proj(x)
+            x = self.mlp_proj(x, flip_out=rc)
             x = F.dropout(x, self.mlp_dropout_rate, training=train)
             x = skip + x
         return x

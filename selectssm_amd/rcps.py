@@ -4,7 +4,11 @@ Same classes, fields and parameter names as the reference's Flax wrappers
 (rcps.py:42-174).  The group action is RC(x)[b, l, d] = x[b, L-1-l, D-1-d]
 (rcps.py:10-19, 37-39).  The wrappers hold no scan of their own: the wrapped
 module (e.g. :class:`~selectssm_amd.BidirectionalMamba`) runs on the HIP
-kernels, and the conjugations here are index flips done by torch on the GPU.
+kernels.  When the wrapped module (or norm) has a ``forward_rc`` method, as this
+package's SelectiveSSM, BidirectionalMamba and norms do, the antisense half runs
+through it: RC(M(RC(x))) computed by index maps in the kernels and permuted
+parameters, with no flipped copy of an activation.  Any other module gets the
+conjugation as materialised flips.
 
 ``module_cls`` / ``norm_cls`` are torch module classes whose instances build
 their parameters from the first input, as Flax modules do (the modules of this
@@ -24,6 +28,14 @@ from .modules import _FlaxModule, lecun_normal_
 def rc_conjugate(x: torch.Tensor) -> torch.Tensor:
     """Flip along the sequence (-2) and channel (-1) axes (rcps.py:37-39)."""
     return torch.flip(x, dims=(-2, -1))
+
+
+def conjugated(module, x, **kwargs):
+    """RC(module(RC(x))) (rcps.py:71): through ``module.forward_rc`` (index maps, no
+    flipped activations) when the module has one, else with materialised flips."""
+    if hasattr(module, "forward_rc"):
+        return module.forward_rc(x, **kwargs)
+    return rc_conjugate(module(rc_conjugate(x), **kwargs))
 
 
 class Dense(_FlaxModule):
@@ -56,13 +68,19 @@ class RMSNorm(_FlaxModule):
         self.epsilon = epsilon
         self.built = False
 
-    def forward(self, x):
+    def forward(self, x, flip: bool = False):
         if not self.built:
             self.scale = torch.nn.Parameter(torch.ones(x.shape[-1], device=x.device))
             self.built = True
         xf = x.float()
-        y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.epsilon) * self.scale
+        scale = self.scale.flip(0) if flip else self.scale
+        y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.epsilon) * scale
         return y.to(x.dtype)
+
+    def forward_rc(self, x):
+        """RC(self(RC(x))): the statistics of a row do not depend on its channel order,
+        so this is the norm with its scale reversed."""
+        return self.forward(x, flip=True)
 
 
 class RCPSWrapper(_FlaxModule):
@@ -79,7 +97,7 @@ class RCPSWrapper(_FlaxModule):
         D = x.shape[-1] // 2
         sense, antisense = x[..., :D], x[..., D:]
         sense_out = self.inner(sense, **kwargs)
-        antisense_out = rc_conjugate(self.inner(rc_conjugate(antisense), **kwargs))
+        antisense_out = conjugated(self.inner, antisense, **kwargs)
         return torch.cat([sense_out, antisense_out], dim=-1)
 
 
@@ -96,7 +114,7 @@ class RCPSNorm(_FlaxModule):
     def forward(self, x, **kwargs):
         D = x.shape[-1] // 2
         sense = self.norm(x[..., :D], **kwargs)
-        antisense = rc_conjugate(self.norm(rc_conjugate(x[..., D:]), **kwargs))
+        antisense = conjugated(self.norm, x[..., D:], **kwargs)
         return torch.cat([sense, antisense], dim=-1)
 
 
@@ -126,8 +144,9 @@ class RCPSEmbedding(_FlaxModule):
     def forward(self, input_ids):
         table = self.embed.embedding
         sense = F.embedding(input_ids, table)
-        rc_ids = torch.flip(self.cmap.to(input_ids.device)[input_ids], dims=(-1,))
-        antisense = rc_conjugate(F.embedding(rc_ids, table))
+        # RC(embed(RC(ids)))[l, d] = table[cmap[ids[l]], D-1-d]: the sequence reversals
+        # cancel and the channel reversal moves onto the (vocab, D) table
+        antisense = F.embedding(self.cmap.to(input_ids.device)[input_ids], table.flip(-1))
         return torch.cat([sense, antisense], dim=-1)
 
 
@@ -153,5 +172,6 @@ class RCPSLMHead(_FlaxModule):
         k = self.kernel.to(x.dtype)
         b = self.bias.to(x.dtype)
         fwd_logits = sense @ k + b
-        rc_logits = torch.flip(antisense, dims=(-1,)) @ k[:, self.cmap.to(x.device)] + b
+        # flip(antisense, channels) @ k[:, cmap] = antisense @ (k with its rows reversed)[:, cmap]
+        rc_logits = antisense @ k.flip(0)[:, self.cmap.to(x.device)] + b
         return fwd_logits + rc_logits

@@ -96,16 +96,26 @@ def _stream():
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
-def _flags(skip, gate, reverse, complement, delta_softplus=False):
+def _flags(skip, gate, reverse, complement, delta_softplus=False, skip_map=None):
+    """desc.flags.  ``reverse`` / ``complement``: the output map (time / channel
+    reversal of the scan position, independently); ``skip_map``: None (the skip's u
+    is read at the output position, the reference's convention) or a (time, channel)
+    pair of bits giving the map of the scan position it is read at instead."""
     f = L.SSM_DELTA_SOFTPLUS if delta_softplus else 0
     if reverse:
         f |= L.SSM_REVERSE
-        if complement:
-            f |= L.SSM_COMPLEMENT
+    if complement:
+        f |= L.SSM_COMPLEMENT
     if skip:
         f |= L.SSM_SKIP
     if gate:
         f |= L.SSM_GATE
+    if skip_map is not None:
+        f |= L.SSM_SKIP_MAP
+        if skip_map[0]:
+            f |= L.SSM_SKIP_REVERSE
+        if skip_map[1]:
+            f |= L.SSM_SKIP_COMPLEMENT
     return f
 
 
@@ -194,17 +204,19 @@ def _scratch(nbytes, device):
 # ------------------------------------------------------------- raw launchers
 
 def scan_fwd(u, delta, A, B, C, Dskip=None, z=None, reverse=False, complement=False, want_ckpt=True,
-             segments=0, delta_softplus=False, y_out=None):
+             segments=0, delta_softplus=False, y_out=None, skip_map=None):
     """Run ``ssm_fwd``.  Tensors on one GPU, I/O dtype shared; u, delta, B, C contiguous,
     ``z`` and ``y_out`` contiguous or row-strided column slices (:func:`row_stride`).
 
     ``segments`` splits each row's time axis (0: chosen from the shape);
     ``delta_softplus``: ``delta`` is the pre-activation and the scan uses
     softplus(delta); ``y_out``: where to write y (allocated if None).  B and C
-    may be column slices of one array (:func:`bc_stride`).
+    may be column slices of one array (:func:`bc_stride`).  ``reverse`` /
+    ``complement`` map the output (independently) and ``skip_map`` the skip's
+    source (:func:`_flags`).
     Returns ``(y, ckpt)``; ``ckpt`` is None when ``want_ckpt`` is False.
     """
-    flags = _flags(Dskip is not None, z is not None, reverse, complement, delta_softplus)
+    flags = _flags(Dskip is not None, z is not None, reverse, complement, delta_softplus, skip_map)
     y = torch.empty_like(u) if y_out is None else y_out
     ld_y, ld_z = row_stride(y), (row_stride(z) if z is not None else 0)
     if ld_y is None or ld_z is None:
@@ -219,13 +231,13 @@ def scan_fwd(u, delta, A, B, C, Dskip=None, z=None, reverse=False, complement=Fa
 
 
 def scan_bwd(u, delta, A, B, C, Dskip, z, ckpt, dy, reverse=False, complement=False, segments=0,
-             delta_softplus=False, dbc_out=None):
+             delta_softplus=False, dbc_out=None, skip_map=None):
     """Run ``ssm_bwd``.  Returns ``(du, ddelta, dA, dB, dC, dD, dz)`` (dD / dz None when unused);
     with ``delta_softplus``, ``ddelta`` is the gradient w.r.t. the pre-activation.
     ``dy`` and ``z`` may be row-strided column slices; dz is always contiguous.  When
     B and C are column slices of one array, dB and dC are the matching slices of
     ``dbc_out`` (or of a new array of that width)."""
-    flags = _flags(Dskip is not None, z is not None, reverse, complement, delta_softplus)
+    flags = _flags(Dskip is not None, z is not None, reverse, complement, delta_softplus, skip_map)
     ld_y, ld_z = row_stride(dy), (row_stride(z) if z is not None else 0)
     if ld_y is None or ld_z is None:
         raise ValueError("dy and z must be contiguous or column slices of a contiguous (B, L, W) tensor")
@@ -258,7 +270,7 @@ def scan_fwd_pair(calls):
         u, delta, A, B, C = c["u"], c["delta"], c["A"], c["B"], c["C"]
         Dskip, z = c.get("Dskip"), c.get("z")
         flags = _flags(Dskip is not None, z is not None, c.get("reverse", False), c.get("complement", False),
-                       c.get("delta_softplus", False))
+                       c.get("delta_softplus", False), c.get("skip_map"))
         y = torch.empty_like(u) if c.get("y_out") is None else c["y_out"]
         ld_y, ld_z = row_stride(y), (row_stride(z) if z is not None else 0)
         if ld_y is None or ld_z is None:
@@ -287,7 +299,7 @@ def scan_bwd_pair(calls):
         u, delta, A, B, C, dy = c["u"], c["delta"], c["A"], c["B"], c["C"], c["dy"]
         Dskip, z = c.get("Dskip"), c.get("z")
         flags = _flags(Dskip is not None, z is not None, c.get("reverse", False), c.get("complement", False),
-                       c.get("delta_softplus", False))
+                       c.get("delta_softplus", False), c.get("skip_map"))
         ld_y, ld_z = row_stride(dy), (row_stride(z) if z is not None else 0)
         if ld_y is None or ld_z is None:
             raise ValueError("dy and z must be contiguous or column slices of a contiguous (B, L, W) tensor")

@@ -76,8 +76,8 @@ static void invalid_descs() {
       {"seqlen -1", [](ssm_desc_t& d) { d.seqlen = -1; }},
       {"dstate 33", [](ssm_desc_t& d) { d.dstate = 33; }},
       {"dtype 9", [](ssm_desc_t& d) { d.dtype = 9; }},
-      {"flags 64", [](ssm_desc_t& d) { d.flags = 64; }},
-      {"complement alone", [](ssm_desc_t& d) { d.flags = SSM_COMPLEMENT; }},
+      {"skip-map bits without SSM_SKIP_MAP", [](ssm_desc_t& d) { d.flags = SSM_SKIP_REVERSE; }},
+      {"flags 256", [](ssm_desc_t& d) { d.flags = 256; }},
       {"delta_broadcast 2", [](ssm_desc_t& d) { d.delta_broadcast = 2; }},
       {"segments 1025", [](ssm_desc_t& d) { d.segments = 1025; }},
       {"ld_y < dim", [](ssm_desc_t& d) { d.ld_y = 3; }},
@@ -174,8 +174,8 @@ static void conv() {
   c.ksize = 9;
   check(ssm_conv_fwd(nullptr, &c, P, (const float*)P, P) == SSM_ERR_INVALID, "conv rejects ksize 9");
   c.ksize = 4;
-  c.flags = SSM_COMPLEMENT;
-  check(ssm_conv_fwd(nullptr, &c, P, (const float*)P, P) == SSM_ERR_INVALID, "conv rejects complement alone");
+  c.flags = SSM_SKIP;
+  check(ssm_conv_fwd(nullptr, &c, P, (const float*)P, P) == SSM_ERR_INVALID, "conv rejects scan-only flags");
   c.flags = 0;
   check(ssm_conv_bwd(nullptr, &c, P, (const float*)P, P, P, (float*)P, nullptr) == SSM_ERR_INVALID,
         "conv backward needs its workspace for dw");

@@ -32,7 +32,8 @@ def test_header_constants_match_binding():
     text = open(HEADER).read()
     consts = dict(re.findall(r"#define (SSM_\w+) (\d+)u?", text))
     for k in ("SSM_OK", "SSM_ERR_INVALID", "SSM_ERR_UNSUPPORTED", "SSM_ERR_HIP", "SSM_F32", "SSM_BF16",
-              "SSM_REVERSE", "SSM_COMPLEMENT", "SSM_SKIP", "SSM_GATE", "SSM_DELTA_SOFTPLUS",
+              "SSM_REVERSE", "SSM_COMPLEMENT", "SSM_SKIP", "SSM_GATE", "SSM_DELTA_SOFTPLUS", "SSM_SKIP_MAP",
+              "SSM_SKIP_REVERSE", "SSM_SKIP_COMPLEMENT",
               "SSM_ACT_NONE", "SSM_ACT_SILU", "SSM_ACT_RELU"):
         assert int(consts[k]) == getattr(L, k), k
     assert int(consts["SSM_ABI_VERSION"]) == L.ABI_VERSION
@@ -89,7 +90,8 @@ def test_split_forward_needs_its_workspace():
 
 @pytest.mark.parametrize("field,value,msg", [
     ("batch", 0, b"batch, seqlen and dim"), ("dstate", 0, b"dstate"), ("dtype", 7, b"dtype"),
-    ("flags", 32, b"unknown flag"), ("flags", 2, b"COMPLEMENT requires"), ("delta_broadcast", 3, b"delta_broadcast"),
+    ("flags", 256, b"unknown flag"), ("flags", 64, b"SKIP_MAP"), ("flags", 128, b"SKIP_MAP"),
+    ("delta_broadcast", 3, b"delta_broadcast"),
     ("segments", -1, b"segments"), ("segments", 1025, b"segments"), ("ld_y", 63, b"ld_y"), ("ld_z", 1, b"ld_z"),
     ("ld_y", 1 << 28, b"seqlen*ld_y"), ("ld_bc", 15, b"ld_bc"), ("ld_bc", 1 << 28, b"ld_bc"),
 ])
@@ -129,7 +131,7 @@ def test_conv_desc_validation():
     long = L.SsmConvDesc(**dict(good, seqlen=128 * 100))
     assert lib.ssm_conv_bwd_workspace_bytes(ctypes.byref(long)) == (200 + 4) * 4 * 64 * 4
     for field, value, msg in [("ksize", 0, b"ksize"), ("ksize", 9, b"ksize"), ("activation", 3, b"activation"),
-                              ("flags", L.SSM_SKIP, b"conv flags"), ("flags", L.SSM_COMPLEMENT, b"COMPLEMENT"),
+                              ("flags", L.SSM_SKIP, b"conv flags"),
                               ("dtype", 5, b"dtype"), ("seqlen", 0, b"seqlen"), ("ld_x", 8, b"ld_x")]:
         bad = L.SsmConvDesc(**{**good, field: value})
         assert lib.ssm_conv_fwd(None, ctypes.byref(bad), p, p, p) == L.SSM_ERR_INVALID, field

@@ -579,3 +579,81 @@ def test_bidirectional_mamba_dt_rank_comes_from_block_width():
     with pytest.raises(ValueError):
         O.bidirectional_mamba_forward(p, x, N, E, dt_rank=math.ceil(ED / 16), tie_in_proj=True, tie_gate=True,
                                       ssm_args={"dt_proj": False})
+
+
+# ------------------------------------------- general index maps (RCPS conjugation)
+
+MAPS = [(False, False), (True, False), (False, True), (True, True)]
+
+
+@pytest.mark.parametrize("tr,cr", MAPS)
+def test_flip_maps_against_index_loops(tr, cr):
+    x = np.random.default_rng(30).standard_normal((2, 5, 4))
+    got = O.flip_maps(x, tr, cr)
+    for b in range(2):
+        for t in range(5):
+            for d in range(4):
+                assert got[b, t, d] == x[b, 4 - t if tr else t, 3 - d if cr else d]
+    assert np.array_equal(O.flip_maps(got, tr, cr), x)
+
+
+@pytest.mark.parametrize("om", MAPS)
+@pytest.mark.parametrize("sm", MAPS + [None])
+def test_block_forward_general_maps_brute_force(om, sm):
+    """y_out[O(t,d)] = (y_scan[t,d] + u[S(t,d)] D[col S(t,d)]) silu(z[O(t,d)]), element by
+    element; S = O when no skip map is given (the reference's skip at the output position)."""
+    x = _rand((2, 11, 5, 3), 14)
+    u, dt, A, B, C, z = (x[k] for k in ("u", "dt", "A", "B", "C", "z"))
+    Dp = np.linspace(0.5, 1.5, 5)
+    got = O.ssm_block_forward(u, dt, A, B, C, Dskip=Dp, z=z, out_map=om, skip_map=sm)
+    ys = O.scan_forward(u, dt, A, B, C)
+    s = om if sm is None else sm
+    ref = np.empty_like(ys)
+    L_, Dn = 11, 5
+    for b in range(2):
+        for t in range(L_):
+            for d in range(Dn):
+                p, q = (L_ - 1 - t if om[0] else t), (Dn - 1 - d if om[1] else d)
+                ts, ds = (L_ - 1 - t if s[0] else t), (Dn - 1 - d if s[1] else d)
+                zz = z[b, p, q]
+                ref[b, p, q] = (ys[b, t, d] + u[b, ts, ds] * Dp[ds]) * zz / (1 + np.exp(-zz))
+    np.testing.assert_allclose(got, ref, rtol=1e-13, atol=1e-15)
+
+
+@pytest.mark.parametrize("rev,comp", [(False, False), (True, False), (True, True)])
+@pytest.mark.parametrize("G", [(True, True), (True, False)])
+def test_conjugated_op_is_the_flipped_module_op(rev, comp, G):
+    """Conjugating SelectiveSSM's epilogue by a flip G (the RC map of an RCPS wrapper, or
+    the time reversal BidirectionalMamba's in_proj leaves behind) keeps the scan and
+    moves the maps: with F the module's flip, output map G o F and skip source F give
+    G(op_F(...)) with the gate read through G as well."""
+    x = _rand((2, 9, 6, 3), 15)
+    u, dt, A, B, C, z = (x[k] for k in ("u", "dt", "A", "B", "C", "z"))
+    Dp = np.linspace(0.5, 1.5, 6)
+    F = (rev, rev and comp)
+    GF = (G[0] != F[0], G[1] != F[1])
+    conj = O.ssm_block_forward(u, dt, A, B, C, Dskip=Dp, z=O.flip_maps(z, *G), out_map=GF, skip_map=F)
+    ref = O.flip_maps(O.ssm_block_forward(u, dt, A, B, C, Dskip=Dp, z=z, reverse=rev, complement=comp), *G)
+    np.testing.assert_allclose(conj, ref, rtol=1e-13, atol=1e-15)
+
+
+@pytest.mark.parametrize("om,sm", [((True, False), (False, False)), ((False, True), (True, False)),
+                                   ((False, False), (True, True)), ((True, True), (False, True))])
+def test_block_backward_general_maps_finite_differences(om, sm):
+    x = _rand((1, 8, 4, 2), 16)
+    Dp = np.linspace(0.5, 1.5, 4)
+    kw = dict(out_map=om, skip_map=sm)
+    grads = O.ssm_block_backward(x["u"], x["dt"], x["A"], x["B"], x["C"], x["g"], Dskip=Dp, z=x["z"], **kw)
+    named = dict(zip(["u", "dt", "A", "B", "C", "D", "z"], grads))
+    x = dict(x, D=Dp)
+
+    def loss(xx):
+        y = O.ssm_block_forward(xx["u"], xx["dt"], xx["A"], xx["B"], xx["C"], Dskip=xx["D"], z=xx["z"], **kw)
+        return float(np.sum(y * x["g"]))
+
+    rng = np.random.default_rng(2)
+    for k in ("u", "dt", "A", "B", "C", "D", "z"):
+        v = rng.standard_normal(np.shape(x[k]))
+        eps = 1e-6
+        fd = (loss(dict(x, **{k: x[k] + eps * v})) - loss(dict(x, **{k: x[k] - eps * v}))) / (2 * eps)
+        assert abs(fd - np.sum(named[k] * v)) <= 1e-6 * max(1.0, abs(fd)), k
