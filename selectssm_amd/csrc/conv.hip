@@ -15,7 +15,12 @@
 // same channels.  Pure HBM streaming: one read of x (plus a K-1 step halo per
 // chunk) and one write of u; the backward reads x and du once and writes dx.
 // dw partial sums are added over the workgroup's waves in LDS and then over
-// workgroups in fixed order, so dw is deterministic.
+// workgroups in fixed order, so dw is deterministic.  dw is a sum over every
+// (batch, step) of the tensor (2^14 terms at BASELINE config 1's width, 2^20 at
+// config 3): its partial sums are accumulated in float64 (each tile's partial
+// rounded once to float32), so its error is a few float32 roundings of the
+// result rather than one per tile; the conv is HBM-bound and the float64 FMAs
+// cost no time there.
 
 #include <hip/hip_runtime.h>
 
@@ -175,13 +180,14 @@ __global__ void __launch_bounds__(kLanes* kCW) conv_bwd_kernel(ConvArgs<T> p) {
     }
   }
   if (p.ws_dw == nullptr) return;  // uniform over the workgroup
-  // dw[k,d] over this thread's steps (dv beyond L is 0), then over the waves
-  __shared__ float sdw[kCW][K][kLanes];
+  // dw[k,d] over this thread's steps (dv beyond L is 0), then over the waves,
+  // in float64
+  __shared__ double sdw[kCW][K][kLanes];
 #pragma unroll
   for (int k = 0; k < K; ++k) {
-    float s = 0.0f;
+    double s = 0.0;
 #pragma unroll
-    for (int i = 0; i < kCT; ++i) s = fmaf(dv[i], xs[i + k], s);
+    for (int i = 0; i < kCT; ++i) s = fma((double)dv[i], (double)xs[i + k], s);
     sdw[wave][k][lane] = s;
   }
   __syncthreads();
@@ -189,10 +195,10 @@ __global__ void __launch_bounds__(kLanes* kCW) conv_bwd_kernel(ConvArgs<T> p) {
     float* __restrict__ out = p.ws_dw + ((int64_t)blockIdx.z * p.ntile + blockIdx.y) * K * D;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-      float s = 0.0f;
+      double s = 0.0;
 #pragma unroll
       for (int w = 0; w < kCW; ++w) s += sdw[w][k][lane];
-      out[(int64_t)k * D + d] = s;
+      out[(int64_t)k * D + d] = (float)s;
     }
   }
 }
@@ -201,8 +207,8 @@ __global__ void __launch_bounds__(kLanes* kCW) conv_bwd_kernel(ConvArgs<T> p) {
 // ws[k*count + i], y = blockIdx.y: a workgroup takes 64 consecutive columns;
 // its 16 lane groups sum the parts k0 + g, k0 + g + 16, ... in order, and the
 // 16 group sums are added in order through LDS (a fixed order overall, so dw
-// is deterministic).  Many parts (long rows) go through two launches: slices
-// of kRedSlice parts into a staging area, then the slices.
+// is deterministic), all in float64.  Many parts (long rows) go through two
+// launches: slices of kRedSlice parts into a staging area, then the slices.
 constexpr int kRedCols = 64, kRedGroups = 16, kRedSlice = 64;
 __global__ void __launch_bounds__(kRedCols* kRedGroups) conv_reduce_kernel(const float* __restrict__ ws,
                                                                           float* __restrict__ out, int nparts,
@@ -213,17 +219,17 @@ __global__ void __launch_bounds__(kRedCols* kRedGroups) conv_reduce_kernel(const
   const int k0 = blockIdx.y * per;
   const int k1 = min(nparts, k0 + per);
   out += (int64_t)blockIdx.y * count;
-  float s = 0.0f;
+  double s = 0.0;
   if (i < count)
-    for (int k = k0 + grp; k < k1; k += kRedGroups) s += ws[(int64_t)k * count + i];
-  __shared__ float part[kRedGroups][kRedCols];
+    for (int k = k0 + grp; k < k1; k += kRedGroups) s += (double)ws[(int64_t)k * count + i];
+  __shared__ double part[kRedGroups][kRedCols];
   part[grp][col] = s;
   __syncthreads();
   if (grp == 0 && i < count) {
-    float t = 0.0f;
+    double t = 0.0;
 #pragma unroll
     for (int g = 0; g < kRedGroups; ++g) t += part[g][col];
-    out[i] = t;
+    out[i] = (float)t;
   }
 }
 

@@ -1,5 +1,5 @@
 """GPU parity of the causal depthwise conv + activation (selectssm.py:167-185)
-against the fp64 oracle (rtol 1e-4 / atol 1e-5 for fp32 I/O; 2e-2 x max|ref|
+against the fp64 oracle (rtol 1e-4 / atol 1e-5 for fp32 I/O, u, dx and dw alike; 2e-2 x max|ref|
 for bf16 I/O, the oracle run on the bf16-rounded inputs).  The flip maps are
 checked bitwise against explicit torch.flip of the input.
 """
@@ -45,7 +45,7 @@ def test_conv_matches_oracle(shape, activation):
     _close("u", u, O.conv_act_forward(x, w2, activation))
     rdx, rdw = O.conv_act_backward(x, w2, g, activation)
     _close("dx", dx, rdx)
-    _close("dw", dw.reshape(K, D), rdw, atol=1e-4)
+    _close("dw", dw.reshape(K, D), rdw)
 
 
 @pytest.mark.parametrize("rev,comp", [(True, False), (True, True)])
@@ -56,7 +56,7 @@ def test_conv_flip_maps_match_oracle(rev, comp):
     _close("u", u, O.conv_act_forward(x, w2, "silu", rev, comp))
     rdx, rdw = O.conv_act_backward(x, w2, g, "silu", rev, comp)
     _close("dx", dx, rdx)
-    _close("dw", dw.reshape(4, 96), rdw, atol=1e-4)
+    _close("dw", dw.reshape(4, 96), rdw)
 
 
 def test_conv_flip_maps_are_exact():
@@ -118,4 +118,5 @@ def test_conv_config1_width():
     _close("u", u, O.conv_act_forward(x, w2, "silu", True, True))
     rdx, rdw = O.conv_act_backward(x, w2, g, "silu", True, True)
     _close("dx", dx, rdx)
-    _close("dw", dw.reshape(4, 2048), rdw, rtol=1e-4, atol=1e-3)
+    # dw sums 2 x 8192 products per entry: its float64 accumulation keeps it at the stated bar
+    _close("dw", dw.reshape(4, 2048), rdw)

@@ -5,8 +5,8 @@ size-independent properties plus a per-row comparison:
   * exact linearity: y(2u) == 2 y(u) and grads(2 dy) == 2 grads(dy), bitwise
     (scaling by 2 commutes with every fp32 rounding in the recurrence);
   * reverse / complement outputs are bitwise flips of the forward output;
-  * batch row 0 against the C port of the reference's custom-VJP algorithm
-    (fp32, oracle/ssm_oracle.c) at rtol 1e-4 / atol 1e-5;
+  * batch row 0 against the C port of the reference's custom-VJP algorithm run
+    in float64 (oracle/ssm_oracle.c) at rtol 1e-4 / atol 1e-5, every output;
   * finiteness of every output.
 """
 import numpy as np
@@ -62,8 +62,8 @@ def test_fullsize_row0_matches_c_port(inputs):
     torch.cuda.synchronize()
     h = {k: x[k][:1].cpu().numpy() for k in ("u", "dt", "B", "C", "g")}
     A = x["A"].cpu().numpy()
-    yr = c_oracle.scan_fwd(h["u"], h["dt"], A, h["B"], h["C"], nthreads=16)
-    gr = c_oracle.scan_bwd(h["u"], h["dt"], A, h["B"], h["C"], h["g"], nthreads=16)
+    yr = c_oracle.scan_fwd(h["u"], h["dt"], A, h["B"], h["C"], nthreads=16, precision="f64")
+    gr = c_oracle.scan_bwd(h["u"], h["dt"], A, h["B"], h["C"], h["g"], nthreads=16, precision="f64")
 
     def close(name, got, ref, rtol=1e-4, atol=1e-5):
         got = got.double().cpu().numpy()
@@ -82,4 +82,4 @@ def test_fullsize_row0_matches_c_port(inputs):
                        x["C"][:1].contiguous())
     g1 = scan_bwd(x["u"][:1].contiguous(), x["dt"][:1].contiguous(), x["A"], x["B"][:1].contiguous(),
                   x["C"][:1].contiguous(), None, None, ck1, x["g"][:1].contiguous())
-    close("dA(row0)", g1[2], gr[2], rtol=1e-4, atol=1e-4)
+    close("dA(row0)", g1[2], gr[2])
