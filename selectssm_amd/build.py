@@ -26,6 +26,7 @@ HIPCC_FLAGS = [
     "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I", os.path.join(REPO_DIR, "include"),
+    "-L/opt/rocm/lib", "-lrocprofiler-sdk-roctx",  # roctx ranges over the C-ABI calls
 ]
 
 

@@ -3,6 +3,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <rocprofiler-sdk-roctx/roctx.h>
 
 #include <cstdint>
 #include <string>
@@ -12,6 +13,16 @@
 namespace ssm {
 
 constexpr float kLog2e = 1.4426950408889634f;
+
+// A roctx range over one C-ABI call (named after the entry point), so a
+// rocprofv3 --marker-trace run attributes every kernel to the call that
+// launched it.  Without a profiler attached the push and pop do nothing.
+struct ApiRange {
+  explicit ApiRange(const char* name) { roctxRangePushA(name); }
+  ~ApiRange() { roctxRangePop(); }
+  ApiRange(const ApiRange&) = delete;
+  ApiRange& operator=(const ApiRange&) = delete;
+};
 
 // Error state of the calling thread (ssm_last_error) and helpers that set it.
 extern thread_local std::string g_last_error;

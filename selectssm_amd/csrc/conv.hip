@@ -366,6 +366,7 @@ size_t ssm_conv_bwd_workspace_bytes(const ssm_conv_desc_t* desc) {
 }
 
 int ssm_conv_fwd(void* stream, const ssm_conv_desc_t* desc, const void* x, const float* w, void* u) {
+  const ApiRange range("ssm_conv_fwd");
   g_last_error.clear();
   ConvShape s;
   if (int rc = validate_conv(desc, &s)) return rc;
@@ -377,6 +378,7 @@ int ssm_conv_fwd(void* stream, const ssm_conv_desc_t* desc, const void* x, const
 
 int ssm_conv_bwd(void* stream, const ssm_conv_desc_t* desc, const void* x, const float* w, const void* du,
                  void* dx, float* dw, void* workspace) {
+  const ApiRange range("ssm_conv_bwd");
   g_last_error.clear();
   ConvShape s;
   if (int rc = validate_conv(desc, &s)) return rc;

@@ -1830,6 +1830,7 @@ size_t ssm_bwd_workspace_bytes(const ssm_desc_t* desc) {
 int ssm_fwd(void* stream, const ssm_desc_t* desc, const void* u, const void* delta, const float* A,
             const void* Bc, const void* Cc, const float* Dskip, const void* z, void* y, float* ckpt,
             void* workspace) {
+  const ApiRange range("ssm_fwd");
   g_last_error.clear();
   Shape s;
   if (int rc = validate(desc, &s)) return rc;
@@ -1846,6 +1847,7 @@ int ssm_fwd(void* stream, const ssm_desc_t* desc, const void* u, const void* del
 int ssm_bwd(void* stream, const ssm_desc_t* desc, const void* u, const void* delta, const float* A,
             const void* Bc, const void* Cc, const float* Dskip, const void* z, const float* ckpt, const void* dy,
             void* du, void* ddelta, float* dA, void* dB, void* dC, float* dD, void* dz, void* workspace) {
+  const ApiRange range("ssm_bwd");
   g_last_error.clear();
   Shape s;
   if (int rc = validate(desc, &s)) return rc;
@@ -1866,6 +1868,7 @@ int ssm_bwd(void* stream, const ssm_desc_t* desc, const void* u, const void* del
 int ssm_bwd_static(void* stream, const ssm_desc_t* desc, const void* u, const void* delta, const float* A,
                    const void* Bc, const void* Cc, const float* Dskip, const void* z, const float* ckpt,
                    const void* dy, void* du, void* ddelta, float* dA, void* dB, void* dC, float* dD, void* dz) {
+  const ApiRange range("ssm_bwd_static");
   g_last_error.clear();
   Shape s;
   if (int rc = validate(desc, &s)) return rc;
@@ -1899,6 +1902,7 @@ static bool same_shape(const ssm_desc_t& a, const ssm_desc_t& b) {
 }
 
 int ssm_fwd_pair(void* stream, const ssm_desc_t* desc, const ssm_fwd_io_t* io) {
+  const ApiRange range("ssm_fwd_pair");
   g_last_error.clear();
   if (desc == nullptr || io == nullptr) return fail(SSM_ERR_INVALID, "ssm_fwd_pair: desc or io is NULL");
   Shape s[2];
@@ -1942,6 +1946,7 @@ int ssm_fwd_pair(void* stream, const ssm_desc_t* desc, const ssm_fwd_io_t* io) {
 }
 
 int ssm_bwd_pair(void* stream, const ssm_desc_t* desc, const ssm_bwd_io_t* io) {
+  const ApiRange range("ssm_bwd_pair");
   g_last_error.clear();
   if (desc == nullptr || io == nullptr) return fail(SSM_ERR_INVALID, "ssm_bwd_pair: desc or io is NULL");
   Shape s[2];
