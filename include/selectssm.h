@@ -69,7 +69,8 @@ typedef struct ssm_desc {
   int64_t dim;            /* D (channels, D_inner) */
   int64_t dstate;         /* N, 1..32 */
   int32_t dtype;          /* SSM_F32 or SSM_BF16 for u, delta, Bc, Cc, z, y, dy, du, ddelta, dB, dC, dz */
-  uint32_t flags;         /* SSM_REVERSE | SSM_COMPLEMENT | SSM_SKIP | SSM_GATE | SSM_DELTA_SOFTPLUS */
+  uint32_t flags;         /* SSM_REVERSE | SSM_COMPLEMENT | SSM_SKIP | SSM_GATE | SSM_DELTA_SOFTPLUS
+                             | SSM_SKIP_MAP (with SSM_SKIP_REVERSE | SSM_SKIP_COMPLEMENT) */
   int32_t delta_broadcast;/* 1: delta is (B,L,1) and shared by all channels */
   int32_t segments;       /* time segments per row: 0 = chosen from the shape, else 1..1024
                              (a row's time axis is split into this many segments that run
