@@ -246,21 +246,26 @@ def main():
 
     K = args.steps
     nd = len(dirs)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(K)]
+    # events: one at the start, then one after each forward and one after each
+    # backward; a step's forward is timed from the previous step's last event
+    # (each recorded event costs the stream a few microseconds, so none is
+    # recorded twice at one point)
+    start = torch.cuda.Event(enable_timing=True)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(K)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    start.record()
     for k in range(K):
-        ev[k][0].record()
         cks = fwd()
-        ev[k][1].record()
+        ev[k][0].record()
         bwd(cks)
-        ev[k][2].record()
+        ev[k][1].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
 
     # per direction (a pair call's time split evenly between its two scans)
-    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / (K * nd)
-    bwd_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / (K * nd)
+    fwd_ms = sum((start if k == 0 else ev[k - 1][1]).elapsed_time(ev[k][0]) for k in range(K)) / (K * nd)
+    bwd_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / (K * nd)
     fwd_b, bwd_b = alg_bytes(B, L, D, N, w, gate=args.gate)
     tokens = B * L * K
     achieved = bwd_b / (bwd_ms * 1e-3) / 1e9

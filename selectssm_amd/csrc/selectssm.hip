@@ -1377,19 +1377,47 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_agg_kernel(BwdArg
   else bwd_agg_body<SPL, EPI, T>(p1, y - rows0);
 }
 
-// out[i] = sum_k ws[k*count + i], k = 0..nparts-1 in order, with element i of
-// the dense sums stored at row i / w, column i % w of an output whose rows are
-// ld elements apart (w = ld: dense).  Each thread sums 4 consecutive outputs
-// with 8 parts' loads in flight; V4 (count and w multiples of 4, ws 16-byte
-// aligned) loads them as float4.
-template <typename TO, bool V4>
-__global__ void reduce_parts_kernel(const float* __restrict__ ws, TO* __restrict__ out, int nparts,
-                                    int64_t count, int64_t w, int64_t ld) {
+// One reduction of the backward's partial sums: out[i] = sum_k part[k*count + i],
+// k = 0..nparts-1 in order, with element i of the dense sums stored at row
+// i / w, column i % w of an output whose rows are ld elements apart (w = ld:
+// dense).  v4: count and w multiples of 4 and part 16-byte aligned (float4
+// loads).  bf16: the output elements are bf16 (else float).
+struct RedJob {
+  const float* part;
+  void* out;
+  int64_t count, w, ld;
+  int nparts, v4, bf16;
+};
+constexpr int kMaxRedJobs = 5;  // dB, dC, dA, dD, broadcast ddelta
+struct RedJobs {
+  RedJob j0, j1, j2, j3, j4;
+};
+// field-wise selects (a dynamically indexed argument struct would be copied
+// to scratch)
+__device__ __forceinline__ RedJob pick_job(const RedJobs& J, int y) {
+  RedJob r;
+#define SSM_JOB(f) r.f = y == 0 ? J.j0.f : y == 1 ? J.j1.f : y == 2 ? J.j2.f : y == 3 ? J.j3.f : J.j4.f;
+  SSM_JOB(part) SSM_JOB(out) SSM_JOB(count) SSM_JOB(w) SSM_JOB(ld) SSM_JOB(nparts) SSM_JOB(v4) SSM_JOB(bf16)
+#undef SSM_JOB
+  return r;
+}
+
+// Every reduction of one backward call in one launch: blockIdx.y selects the
+// job.  Each thread sums 4 consecutive outputs, with kIn parts' loads in
+// flight.
+__global__ void reduce_parts_kernel(RedJobs jobs) {
+  const RedJob jb = pick_job(jobs, blockIdx.y);
   const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
-  if (i0 >= count) return;
+  if (i0 >= jb.count) return;
+  const int64_t w = jb.w, ld = jb.ld, count = jb.count;
+  const float* __restrict__ ws = jb.part;
   auto oidx = [&](int64_t i) { return w == ld ? i : (i / w) * ld + i % w; };
+  auto put = [&](int64_t o, float v) {
+    if (jb.bf16) st(static_cast<bf16*>(jb.out), o, v);
+    else st(static_cast<float*>(jb.out), o, v);
+  };
   constexpr int kIn = 8;
-  if constexpr (V4) {
+  if (jb.v4) {
     float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     auto add = [&](const float4 v) {
       s[0] += v.x;
@@ -1398,23 +1426,23 @@ __global__ void reduce_parts_kernel(const float* __restrict__ ws, TO* __restrict
       s[3] += v.w;
     };
     int k = 0;
-    for (; k + kIn <= nparts; k += kIn) {
+    for (; k + kIn <= jb.nparts; k += kIn) {
       float4 v[kIn];
 #pragma unroll
       for (int j = 0; j < kIn; ++j) v[j] = *reinterpret_cast<const float4*>(ws + (int64_t)(k + j) * count + i0);
 #pragma unroll
       for (int j = 0; j < kIn; ++j) add(v[j]);
     }
-    for (; k < nparts; ++k) add(*reinterpret_cast<const float4*>(ws + (int64_t)k * count + i0));
+    for (; k < jb.nparts; ++k) add(*reinterpret_cast<const float4*>(ws + (int64_t)k * count + i0));
     const int64_t o = oidx(i0);  // the 4 stay in one row (w % 4 == 0)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) st(out, o + e, s[e]);
+    for (int e = 0; e < 4; ++e) put(o + e, s[e]);
   } else {
     const int m = (int)(count - i0 < 4 ? count - i0 : 4);
     for (int e = 0; e < m; ++e) {
       float sum = 0.0f;
-      for (int k = 0; k < nparts; ++k) sum += ws[(int64_t)k * count + i0 + e];
-      st(out, oidx(i0 + e), sum);
+      for (int k = 0; k < jb.nparts; ++k) sum += ws[(int64_t)k * count + i0 + e];
+      put(oidx(i0 + e), sum);
     }
   }
 }
@@ -1485,6 +1513,10 @@ int validate(const ssm_desc_t* desc, Shape* s) {
     return fail(SSM_ERR_INVALID, "seqlen*ld_y and seqlen*ld_z must be <= 2^30");
   if (desc->ld_bc != 0 && (desc->ld_bc < desc->dstate || desc->seqlen * desc->ld_bc > (int64_t(1) << 30)))
     return fail(SSM_ERR_INVALID, "ld_bc must be 0 or >= dstate, with seqlen*ld_bc <= 2^30");
+  // the backward's partial-sum reduction runs one thread per 4 sums of its
+  // largest job (B*L*N for dB and dC, D*N for dA) in a 1-D grid
+  if (std::max(desc->batch * desc->seqlen * desc->dstate, desc->dim * desc->dstate) > (int64_t(1) << 33))
+    return fail(SSM_ERR_INVALID, "batch*seqlen*dstate and dim*dstate must be <= 2^33");
   s->B = (int)desc->batch;
   s->L = (int)desc->seqlen;
   s->D = (int)desc->dim;
@@ -1714,25 +1746,27 @@ int launch_bwd_reduce(hipStream_t st, const ssm_desc_t* desc, const Shape& s, fl
   const bool bcast = desc->delta_broadcast != 0;
   const WsLayout wl = ws_layout(s, bcast);
   float* ws = static_cast<float*>(workspace);
-  auto reduce = [&](const float* part, auto* out, int nparts, int64_t count, int64_t w, int64_t ld) {
-    using TO = std::remove_pointer_t<decltype(out)>;
-    const int threads = 256;
-    const int64_t blocks = ((count + 3) / 4 + threads - 1) / threads;
-    if (count % 4 == 0 && w % 4 == 0 && reinterpret_cast<uintptr_t>(part) % 16 == 0)
-      hipLaunchKernelGGL((reduce_parts_kernel<TO, true>), dim3((unsigned)blocks), dim3(threads), 0, st, part,
-                         out, nparts, count, w, ld);
-    else
-      hipLaunchKernelGGL((reduce_parts_kernel<TO, false>), dim3((unsigned)blocks), dim3(threads), 0, st, part,
-                         out, nparts, count, w, ld);
+  RedJob job[kMaxRedJobs] = {};
+  int njobs = 0;
+  int64_t maxcount = 0;
+  auto reduce = [&](const float* part, void* out, bool out_bf16, int nparts, int64_t count, int64_t w, int64_t ld) {
+    const bool v4 = count % 4 == 0 && w % 4 == 0 && reinterpret_cast<uintptr_t>(part) % 16 == 0;
+    job[njobs++] = RedJob{part, out, count, w, ld, nparts, v4 ? 1 : 0, out_bf16 ? 1 : 0};
+    maxcount = std::max(maxcount, count);
   };
+  constexpr bool kBf16 = std::is_same_v<T, bf16>;
   const int64_t bln = (int64_t)s.B * s.L * s.N;
   const int64_t dn = (int64_t)s.D * s.N;
   const int64_t bl = (int64_t)s.B * s.L;
-  reduce(ws + wl.dB, static_cast<T*>(dB), s.ncb, bln, s.N, s.ldbc);
-  reduce(ws + wl.dC, static_cast<T*>(dC), s.ncb, bln, s.N, s.ldbc);
-  reduce(ws + wl.dA, dA, s.B * s.nseg, dn, dn, dn);
-  if (desc->flags & SSM_SKIP) reduce(ws + wl.dD, dD, s.B * s.nseg, (int64_t)s.D, s.D, s.D);
-  if (bcast) reduce(ws + wl.ddt, static_cast<T*>(ddelta), s.ncb, bl, bl, bl);
+  reduce(ws + wl.dB, dB, kBf16, s.ncb, bln, s.N, s.ldbc);
+  reduce(ws + wl.dC, dC, kBf16, s.ncb, bln, s.N, s.ldbc);
+  reduce(ws + wl.dA, dA, false, s.B * s.nseg, dn, dn, dn);
+  if (desc->flags & SSM_SKIP) reduce(ws + wl.dD, dD, false, s.B * s.nseg, (int64_t)s.D, s.D, s.D);
+  if (bcast) reduce(ws + wl.ddt, ddelta, kBf16, s.ncb, bl, bl, bl);
+  const RedJobs jobs{job[0], job[1], job[2], job[3], job[4]};
+  const int threads = 256;
+  const int64_t blocks = ((maxcount + 3) / 4 + threads - 1) / threads;
+  hipLaunchKernelGGL(reduce_parts_kernel, dim3((unsigned)blocks, (unsigned)njobs), dim3(threads), 0, st, jobs);
   return hip_check(hipGetLastError(), "ssm_bwd reduce launch");
 }
 

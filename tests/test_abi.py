@@ -105,6 +105,19 @@ def test_invalid_desc_is_rejected_before_any_launch(field, value, msg):
     assert msg in lib.ssm_last_error()
 
 
+def test_reduction_grid_bound_is_checked_before_any_launch():
+    """B*L*N above 2^33 (each extent valid on its own) is refused up front: the
+    backward's partial-sum reduction grid would not fit a 1-D launch."""
+    lib = L.lib()
+    d = L.make_desc(65535, 1 << 20, 64, 16)
+    p = ctypes.c_void_p(16)
+    rc = lib.ssm_bwd(None, ctypes.byref(d), p, p, p, p, p, None, None, p, p, p, p, p, p, p, None, None, p)
+    assert rc == L.SSM_ERR_INVALID
+    assert b"batch*seqlen*dstate" in lib.ssm_last_error()
+    d = L.make_desc(8192, 1 << 16, 64, 16)  # 2^33 sums: the bound itself is accepted
+    assert lib.ssm_bwd_workspace_bytes(ctypes.byref(d)) > 0
+
+
 def test_null_pointers_and_missing_epilogue_operands_are_rejected():
     lib = L.lib()
     d = L.make_desc(2, 64, 64, 16)
