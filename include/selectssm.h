@@ -182,11 +182,12 @@ typedef struct {
  * (resp. ssm_bwd) called for each in turn.  Replaces the forward and reverse
  * SSM calls of BidirectionalMamba (selectssm.py:325-326): when both descs
  * have the same shape (batch, seqlen, dim, dstate, dtype, delta_broadcast,
- * segments and SSM_DELTA_SOFTPLUS), the two scans run as one launch of each
- * kernel: the time-split aggregate passes always, the main passes when the
+ * segments and SSM_DELTA_SOFTPLUS), the two scans share launches: the
+ * time-split aggregate passes always, and ssm_fwd_pair's main pass when the
  * two also need the same kernel variant (both with or both without the
- * epilogue staging of SSM_GATE / reverse SSM_SKIP; forward: u and delta both
- * 16-byte aligned or both not).  Each call keeps its own time segments, so the
+ * epilogue staging of SSM_GATE / reverse SSM_SKIP; u and delta both 16-byte
+ * aligned or both not).  ssm_bwd_pair's main passes run one launch per call
+ * (a joint one gained nothing).  Each call keeps its own time segments, so the
  * results are bitwise those of the two calls.  The two calls must not share
  * an output or workspace buffer, and must have the same dtype.
  */

@@ -73,6 +73,14 @@ constexpr int kTT = SSM_FWD_TT;  // forward time tile
 #define SSM_CK 16
 #endif
 constexpr int kCK = SSM_CK;   // checkpoint interval = backward block length
+// ssm_bwd_pair: 1 runs both calls' main passes as one launch when they allow it;
+// 0 (default) one launch per call.  The backward already has two waves per SIMD
+// with one call: the joint launch measured equal at op level (config 2) and
+// 0.2 ms slower per BidirectionalMamba step (config-2 module, gated build).
+// The aggregate passes of a pair always share a launch.
+#ifndef SSM_PAIR_JOINT_BWD_MAIN
+#define SSM_PAIR_JOINT_BWD_MAIN 0
+#endif
 #ifndef SSM_FWD_PF
 #define SSM_FWD_PF 2
 #endif
@@ -2006,7 +2014,12 @@ int ssm_bwd_pair(void* stream, const ssm_desc_t* desc, const ssm_bwd_io_t* io) {
     if (same) {
       if (s[0].nseg > 1)
         if (int rc = launch_bwd_agg<T>(st, s[0], a[0], a[1], 2 * s[0].B)) return rc;
-      if (int rc = launch_bwd_main<T>(st, &desc[0], s[0], a[0], a[1], 2 * s[0].B)) return rc;
+      if (SSM_PAIR_JOINT_BWD_MAIN) {
+        if (int rc = launch_bwd_main<T>(st, &desc[0], s[0], a[0], a[1], 2 * s[0].B)) return rc;
+      } else {
+        for (int k = 0; k < 2; ++k)
+          if (int rc = launch_bwd_main<T>(st, &desc[k], s[k], a[k], a[k], s[k].B)) return rc;
+      }
     } else {
       for (int k = 0; k < 2; ++k) {
         if (s[k].nseg > 1)

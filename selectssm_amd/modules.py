@@ -97,6 +97,19 @@ class Dense(torch.nn.Module):
         y = _DenseFn.apply(x2, w, b)
         return y.reshape(*x.shape[:-1], w.shape[1])
 
+    def forward_split(self, x, widths, flip_in: bool = False):
+        """The output's consecutive column blocks of the given widths (views of
+        one output array), as ``jnp.split(dense(x), ...)`` gives them; the
+        backward consumes the blocks' gradients without assembling the full
+        width (:class:`_DenseSplitFn`)."""
+        w = self.kernel.to(x.dtype)
+        b = None if self.bias is None else self.bias.to(x.dtype)
+        if flip_in:
+            w = w.flip(0)
+        x2 = x.reshape(-1, x.shape[-1])
+        blocks = _DenseSplitFn.apply(x2, w, b, *widths)
+        return tuple(h.view(*x.shape[:-1], h.shape[-1]) for h in blocks)
+
 
 class _DenseFn(torch.autograd.Function):
     """x2 @ w + b with the weight gradient through _tn (split over the rows)."""
@@ -266,29 +279,56 @@ def _core_param_grads(saved, grads, dbc, N, rank):
     return du, dA_log, f32(dWbc), f32(dbbc), f32(dWdt), f32(dbdt), dWp, dbp, dD, dz
 
 
-class _SplitCols(torch.autograd.Function):
-    """Consecutive column blocks of ``h`` (``jnp.split`` of in_proj's output,
-    selectssm.py:319), returned as views.  Slicing ``h`` directly gives each
-    block a zero-filled gradient of h's full shape, which autograd then adds
-    up; this backward writes the blocks' gradients side by side into one."""
+class _DenseSplitFn(torch.autograd.Function):
+    """h2 = x2 @ w + b returned as its consecutive column blocks (in_proj followed
+    by the ``jnp.split`` of selectssm.py:319), each a view of h2.  The backward
+    takes the blocks' gradients as they come: dx = sum_i g_i @ w_i^T accumulates
+    block by block, and dw, db are built per block, so no gradient of h2's full
+    width is ever assembled (slicing h2 would give each block a zero-filled
+    full-width gradient to add up; concatenating the blocks' gradients would
+    copy them all once more)."""
 
     @staticmethod
-    def forward(ctx, h, *widths):
-        if sum(widths) != h.shape[-1]:
-            raise ValueError(f"column blocks {widths} do not cover the last dimension {h.shape[-1]}")
+    def forward(ctx, x2, w, b, *widths):
+        if sum(widths) != w.shape[1]:
+            raise ValueError(f"column blocks {widths} do not cover the {w.shape[1]} outputs")
+        ctx.save_for_backward(x2, w)
         ctx.widths = widths
+        ctx.has_bias = b is not None
+        h2 = x2 @ w if b is None else torch.addmm(b, x2, w)
         outs, o = [], 0
-        for w in widths:
-            outs.append(h[..., o:o + w])
-            o += w
+        for wd in widths:
+            outs.append(h2[:, o:o + wd])
+            o += wd
         return tuple(outs)
 
     @staticmethod
     def backward(ctx, *grads):
-        ref = next(g for g in grads if g is not None)
-        parts = [g if g is not None else torch.zeros(*ref.shape[:-1], w, dtype=ref.dtype, device=ref.device)
-                 for g, w in zip(grads, ctx.widths)]
-        return (torch.cat(parts, dim=-1), *([None] * len(ctx.widths)))
+        x2, w = ctx.saved_tensors
+        dx = None
+        dw_parts, db_parts, o = [], [], 0
+        for g, wd in zip(grads, ctx.widths):
+            wb = w[:, o:o + wd]
+            o += wd
+            if g is None:  # an unused block: zero gradient
+                dw_parts.append(torch.zeros_like(wb))
+                db_parts.append(torch.zeros(wd, dtype=w.dtype, device=w.device))
+                continue
+            g = g.contiguous()
+            if ctx.needs_input_grad[0]:
+                if dx is None:
+                    dx = g @ wb.t()
+                else:
+                    dx.addmm_(g, wb.t())
+            if ctx.needs_input_grad[1]:
+                dw_parts.append(_tn(x2, g))
+            if ctx.has_bias and ctx.needs_input_grad[2]:
+                db_parts.append(g.sum(0))
+        if dx is None and ctx.needs_input_grad[0]:
+            dx = torch.zeros_like(x2)
+        dw = torch.cat(dw_parts, dim=1) if ctx.needs_input_grad[1] else None
+        db = torch.cat(db_parts) if ctx.has_bias and ctx.needs_input_grad[2] else None
+        return (dx, dw, db, *([None] * len(ctx.widths)))
 
 
 class _SSMCoreFn(torch.autograd.Function):
@@ -789,11 +829,10 @@ class BidirectionalMamba(_FlaxModule):
             x = self.RMSNorm_0(x, flip=rc)
         ED = self.ED
         n_in = 1 if self.tie_in_proj else 2
-        h = self.in_proj(x, flip_in=rc)
         conj = TIME_MAP if rc else None
-        # jnp.split at [ED, n_in*ED, (n_in+1)*ED] (selectssm.py:319-321)
+        # in_proj, then jnp.split at [ED, n_in*ED, (n_in+1)*ED] (selectssm.py:319-321)
         n_gate = 1 if self.tie_gate else 2
-        blocks = _SplitCols.apply(h, *([ED] * (n_in + n_gate)))
+        blocks = self.in_proj.forward_split(x, [ED] * (n_in + n_gate), flip_in=rc)
         xf, zf = blocks[0], blocks[n_in]
         xr = xf if self.tie_in_proj else blocks[1]
         zr = zf if self.tie_gate else blocks[n_in + 1]

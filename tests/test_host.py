@@ -122,20 +122,30 @@ def test_split_weight_gradient_product(K, M, N, dtype):
     assert torch.allclose(got.double(), ref, rtol=tol, atol=tol * float(ref.abs().max()))
 
 
-def test_split_columns_views_and_gradient():
-    """in_proj's output split into column blocks: the blocks are views of h, and
-    the gradient of h is the blocks' gradients side by side (zeros for an unused block)."""
-    from selectssm_amd.modules import _SplitCols
+def test_dense_split_views_and_gradient():
+    """in_proj followed by its column split (selectssm.py:319): the blocks are views
+    of one output, and the gradients (x, kernel, bias) equal those of the unsplit
+    product sliced by the same blocks, with an unused block contributing zero."""
+    from selectssm_amd.modules import _DenseSplitFn
 
-    h = torch.randn(2, 5, 12, dtype=torch.float64, requires_grad=True)
-    a, b, c = _SplitCols.apply(h, 4, 4, 4)
-    assert a.data_ptr() == h.data_ptr() and c.data_ptr() == h.data_ptr() + 8 * 8
-    (2 * a.sum() + (c * c).sum()).backward()
-    ref = torch.zeros_like(h)
-    ref[..., :4] = 2
-    ref[..., 8:] = 2 * h.detach()[..., 8:]
-    assert torch.equal(h.grad, ref)
-    assert torch.autograd.gradcheck(lambda t: _SplitCols.apply(t, 3, 9),
-                                    (torch.randn(2, 3, 12, dtype=torch.float64, requires_grad=True),))
+    g = torch.Generator().manual_seed(5)
+    x2 = torch.randn(10, 6, dtype=torch.float64, generator=g, requires_grad=True)
+    w = torch.randn(6, 12, dtype=torch.float64, generator=g, requires_grad=True)
+    b = torch.randn(12, dtype=torch.float64, generator=g, requires_grad=True)
+    a, m, c = _DenseSplitFn.apply(x2, w, b, 4, 3, 5)
+    assert a.data_ptr() + 4 * 8 == m.data_ptr() and m.data_ptr() + 3 * 8 == c.data_ptr()
+    assert a.stride() == (12, 1)
+    (2 * a.sum() + (c * c).sum()).backward()  # the middle block unused
+    got = (x2.grad.clone(), w.grad.clone(), b.grad.clone())
+    for t in (x2, w, b):
+        t.grad = None
+    h = x2 @ w + b
+    (2 * h[:, :4].sum() + (h[:, 7:] ** 2).sum()).backward()
+    for u, v in zip(got, (x2.grad, w.grad, b.grad)):
+        assert torch.allclose(u, v, rtol=1e-12, atol=1e-12)
+    assert torch.autograd.gradcheck(lambda xx, ww, bb: _DenseSplitFn.apply(xx, ww, bb, 3, 9),
+                                    (torch.randn(4, 3, dtype=torch.float64, requires_grad=True),
+                                     torch.randn(3, 12, dtype=torch.float64, requires_grad=True),
+                                     torch.randn(12, dtype=torch.float64, requires_grad=True)))
     with pytest.raises(ValueError):
-        _SplitCols.apply(h, 4, 4)
+        _DenseSplitFn.apply(x2, w, b, 4, 4)
