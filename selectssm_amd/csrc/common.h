@@ -177,21 +177,29 @@ __device__ __forceinline__ float sigmoid(float x) {
   return fast_rcp(1.0f + fast_exp2(-x * kLog2e));
 }
 
-// log(1 + y) for y >= 0 as log(u) * y / (u - 1) with u = fl(1 + y): the
-// rounding of 1 + y cancels in the ratio (Goldberg, "What every computer
-// scientist should know about floating-point arithmetic", 1991, Theorem 4);
-// log(u) is v_log_f32 (log2) times ln 2
-__device__ __forceinline__ float log1p_nonneg(float y) {
-  constexpr float kLn2 = 0.6931471805599453f;
-  const float u = 1.0f + y;
-  const float d = u - 1.0f;
-  return d == 0.0f ? y : __builtin_amdgcn_logf(u) * kLn2 * (y * fast_rcp(d));
+// softplus(x) = log(1 + e^x) = max(x, 0) + log1p(e), e = e^-|x|, as
+// jax.nn.softplus (logaddexp(x, 0)) defines it.  With u = fl(1 + e),
+// log1p(e) = log(u) + log(1 + d / u) for d = e - (u - 1), which is exact
+// (u - 1 is exact for u in [1, 2]; then e and u - 1 are within a factor 2 of
+// each other, or u = 1 and d = e).  |d| <= 2^-24 u, so log(1 + d / u) is d / u
+// to within 2^-48; softplus takes d itself for d / u (an error of at most
+// |d| e / u, under 1.5 ulp of log1p(e)), softplus_sigmoid multiplies by the
+// 1 / u it needs anyway.  log(u) is v_log_f32 (log2) times ln 2.
+constexpr float kLn2 = 0.6931471805599453f;
+__device__ __forceinline__ float softplus(float x) {
+  const float e = fast_exp2(-fabsf(x) * kLog2e);
+  const float u = 1.0f + e;
+  return fmaxf(x, 0.0f) + fmaf(__builtin_amdgcn_logf(u), kLn2, e - (u - 1.0f));
 }
 
-// softplus(x) = log(1 + e^x) = max(x, 0) + log1p(e^-|x|), as jax.nn.softplus
-// (logaddexp(x, 0)) defines it
-__device__ __forceinline__ float softplus(float x) {
-  return fmaxf(x, 0.0f) + log1p_nonneg(fast_exp2(-fabsf(x) * kLog2e));
+// softplus(x) and its derivative sigmoid(x) (into *sg) from one exp and one
+// rcp: sigmoid(x) = 1 / u for x >= 0 and e / u below
+__device__ __forceinline__ float softplus_sigmoid(float x, float* sg) {
+  const float e = fast_exp2(-fabsf(x) * kLog2e);
+  const float u = 1.0f + e;
+  const float r = fast_rcp(u);
+  *sg = x >= 0.0f ? r : e * r;
+  return fmaxf(x, 0.0f) + fmaf(__builtin_amdgcn_logf(u), kLn2, (e - (u - 1.0f)) * r);
 }
 
 // ------------------------------------------------------ cross-lane reductions

@@ -913,10 +913,7 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
       const int i = srow0 + k * RSTEP;
       const bool in = svalid && t0 + i < L;
       float dtv = val(r_dt[k]), sg = 1.0f;
-      if constexpr (decltype(sp_tag)::value) {
-        sg = sigmoid(dtv);
-        dtv = softplus(dtv);
-      }
+      if constexpr (decltype(sp_tag)::value) dtv = softplus_sigmoid(dtv, &sg);
       const float go = in ? val(r_dy[k]) : 0.0f;
       float dyg = go;
       if (gate) {
