@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define SSM_ABI_VERSION 7
+#define SSM_ABI_VERSION 8
 
 /* error codes */
 #define SSM_OK 0
@@ -62,6 +62,12 @@ extern "C" {
                                    flip (selectssm.py:167-168) */
 #define SSM_SKIP_REVERSE 64u    /* with SSM_SKIP_MAP: S reverses time, t -> L-1-t */
 #define SSM_SKIP_COMPLEMENT 128u /* with SSM_SKIP_MAP: S mirrors channels, d -> D-1-d */
+#define SSM_ACCUMULATE 256u     /* backward only (ssm_fwd ignores it): ssm_bwd adds the gate's
+                                   gradient to dz (which then holds valid data) instead of
+                                   writing it; needs SSM_GATE.  In a conv desc, ssm_conv_bwd adds
+                                   to dx.  For inputs two calls share: BidirectionalMamba's tied
+                                   gate and in_proj blocks (selectssm.py:320-321) get one gradient
+                                   buffer, the second call accumulating into it */
 
 typedef struct ssm_desc {
   int64_t batch;          /* B */
@@ -70,7 +76,8 @@ typedef struct ssm_desc {
   int64_t dstate;         /* N, 1..32 */
   int32_t dtype;          /* SSM_F32 or SSM_BF16 for u, delta, Bc, Cc, z, y, dy, du, ddelta, dB, dC, dz */
   uint32_t flags;         /* SSM_REVERSE | SSM_COMPLEMENT | SSM_SKIP | SSM_GATE | SSM_DELTA_SOFTPLUS
-                             | SSM_SKIP_MAP (with SSM_SKIP_REVERSE | SSM_SKIP_COMPLEMENT) */
+                             | SSM_SKIP_MAP (with SSM_SKIP_REVERSE | SSM_SKIP_COMPLEMENT)
+                             | SSM_ACCUMULATE */
   int32_t delta_broadcast;/* 1: delta is (B,L,1) and shared by all channels */
   int32_t segments;       /* time segments per row: 0 = chosen from the shape, else 1..1024
                              (a row's time axis is split into this many segments that run
@@ -189,7 +196,10 @@ typedef struct {
  * aligned or both not).  ssm_bwd_pair's main passes run one launch per call
  * (a joint one gained nothing).  Each call keeps its own time segments, so the
  * results are bitwise those of the two calls.  The two calls must not share
- * an output or workspace buffer, and must have the same dtype.
+ * an output or workspace buffer, and must have the same dtype, with one
+ * exception in ssm_bwd_pair: when the second call has SSM_ACCUMULATE, both may
+ * name one dz buffer, which then receives the first call's dz plus the
+ * second's (the two main passes run in call order).
  */
 int ssm_fwd_pair(void* stream, const ssm_desc_t* desc, const ssm_fwd_io_t* io);
 int ssm_bwd_pair(void* stream, const ssm_desc_t* desc, const ssm_bwd_io_t* io);
@@ -217,7 +227,8 @@ typedef struct ssm_conv_desc {
   int64_t dim;            /* D */
   int32_t ksize;          /* K (shift_conv_size), 1..8 */
   int32_t dtype;          /* SSM_F32 or SSM_BF16 for x, u, du, dx; w and dw are f32 */
-  uint32_t flags;         /* SSM_REVERSE (time) | SSM_COMPLEMENT (channel), either or both */
+  uint32_t flags;         /* SSM_REVERSE (time) | SSM_COMPLEMENT (channel), either or both;
+                             SSM_ACCUMULATE: ssm_conv_bwd adds to dx */
   int32_t activation;     /* SSM_ACT_* */
   int64_t ld_x;           /* elements between consecutive time rows of x; 0 = dim (x may be a
                              column slice of in_proj's output, selectssm.py:319); dx is always

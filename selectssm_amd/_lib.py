@@ -26,12 +26,13 @@ SSM_DELTA_SOFTPLUS = 16
 SSM_SKIP_MAP = 32
 SSM_SKIP_REVERSE = 64
 SSM_SKIP_COMPLEMENT = 128
+SSM_ACCUMULATE = 256
 
 SSM_ACT_NONE = 0
 SSM_ACT_SILU = 1
 SSM_ACT_RELU = 2
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 STATIC_SCRATCH_BYTES = 64 << 20  # SSM_STATIC_SCRATCH_BYTES: ssm_bwd_static's workspace
 

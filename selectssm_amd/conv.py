@@ -25,10 +25,11 @@ def _act_code(activation):
     return _ACTS[activation]
 
 
-def _conv_desc(x, K, reverse, complement, activation):
-    """``reverse`` / ``complement``: time and channel reversal of x's index map, independently."""
+def _conv_desc(x, K, reverse, complement, activation, accumulate=False):
+    """``reverse`` / ``complement``: time and channel reversal of x's index map, independently;
+    ``accumulate``: the backward adds to dx (SSM_ACCUMULATE)."""
     Bt, Ln, D = x.shape
-    flags = 0
+    flags = L.SSM_ACCUMULATE if accumulate else 0
     if reverse:
         flags |= L.SSM_REVERSE
     if complement:
@@ -54,11 +55,17 @@ def conv_fwd(x, w, reverse=False, complement=False, activation="silu"):
     return u
 
 
-def conv_bwd(x, w, du, reverse=False, complement=False, activation="silu", need_dx=True, need_dw=True):
-    """(dx, dw) of :func:`conv_fwd` (``ssm_conv_bwd``); either may be skipped (None)."""
-    desc = _conv_desc(x, w.shape[0], reverse, complement, activation)
+def conv_bwd(x, w, du, reverse=False, complement=False, activation="silu", need_dx=True, need_dw=True,
+             dx_out=None, accumulate=False):
+    """(dx, dw) of :func:`conv_fwd` (``ssm_conv_bwd``); either may be skipped (None).
+    ``dx_out``: the (B, L, D) array to write dx into, or with ``accumulate`` to add it to."""
+    if accumulate and (dx_out is None or not need_dx):
+        raise ValueError("accumulate needs dx_out")
+    desc = _conv_desc(x, w.shape[0], reverse, complement, activation, accumulate)
     lib = L.lib()
-    dx = torch.empty(x.shape, dtype=x.dtype, device=x.device) if need_dx else None
+    if dx_out is not None and (dx_out.shape != x.shape or dx_out.dtype != x.dtype or not dx_out.is_contiguous()):
+        raise ValueError("dx_out must be a contiguous array of x's shape and dtype")
+    dx = (dx_out if dx_out is not None else torch.empty(x.shape, dtype=x.dtype, device=x.device)) if need_dx else None
     dw = torch.empty_like(w) if need_dw else None
     ws = _scratch(L.size_query(lib.ssm_conv_bwd_workspace_bytes, desc), x.device) if need_dw else None
     L.check(lib.ssm_conv_bwd(_stream(), ctypes.byref(desc), _ptr(x), _ptr(w), _ptr(du), _ptr(dx), _ptr(dw),
@@ -79,6 +86,55 @@ class ConvActFn(torch.autograd.Function):
         dx, dw = conv_bwd(x, w, du.to(x.dtype).contiguous(), *ctx.cfg, need_dx=ctx.needs_input_grad[0],
                           need_dw=ctx.needs_input_grad[1])
         return dx, dw, None, None, None
+
+
+class ConvActPairFn(torch.autograd.Function):
+    """Two convs of one input x (BidirectionalMamba with tie_in_proj feeds xf to
+    both directions, selectssm.py:320): the backward writes the first conv's dx
+    and adds the second's to it in its kernel (SSM_ACCUMULATE), instead of two dx
+    arrays summed afterwards.  The sum is the same: one fp32 addition per element."""
+
+    @staticmethod
+    def forward(ctx, x, w1, w2, cfg1, cfg2):
+        ctx.save_for_backward(x, w1, w2)
+        ctx.cfg = (cfg1, cfg2)
+        return conv_fwd(x, w1, *cfg1), conv_fwd(x, w2, *cfg2)
+
+    @staticmethod
+    def backward(ctx, du1, du2):
+        x, w1, w2 = ctx.saved_tensors
+        cfg1, cfg2 = ctx.cfg
+        need_dx = ctx.needs_input_grad[0]
+        dx = None
+        dw = []
+        for du, w, cfg, need_dw in ((du1, w1, cfg1, ctx.needs_input_grad[1]), (du2, w2, cfg2, ctx.needs_input_grad[2])):
+            if du is None:
+                dw.append(None)
+                continue
+            d, g = conv_bwd(x, w, du.to(x.dtype).contiguous(), *cfg, need_dx=need_dx, need_dw=need_dw, dx_out=dx,
+                            accumulate=dx is not None)
+            dx = d if need_dx else None
+            dw.append(g)
+        return dx, dw[0], dw[1], None, None
+
+
+def conv1d_act_pair(x, w1, w2, map1, map2, activation1="silu", activation2="silu"):
+    """The two convs of one input, :func:`conv1d_act_map` with (time, channel) maps
+    ``map1`` and ``map2``, whose x-gradients are summed inside the second backward kernel."""
+    if x.dim() != 3:
+        raise ValueError(f"x must be (B, L, D), got shape {tuple(x.shape)}")
+    if not (x.is_cuda and w1.is_cuda and w2.is_cuda):
+        raise ValueError("conv1d_act inputs must be GPU tensors (there is no CPU path)")
+    if x.dtype not in _IO_DTYPES:
+        raise TypeError(f"conv1d_act supports float32 and bfloat16 activations, got {x.dtype}")
+    _act_code(activation1)
+    _act_code(activation2)
+    D = x.shape[-1]
+    w1 = _weight(w1, D).to(torch.float32).contiguous()
+    w2 = _weight(w2, D).to(torch.float32).contiguous()
+    cfg1 = (bool(map1[0]), bool(map1[1]), activation1)
+    cfg2 = (bool(map2[0]), bool(map2[1]), activation2)
+    return ConvActPairFn.apply(as_rows(x, x.dtype)[0], w1, w2, cfg1, cfg2)
 
 
 def conv1d_act(x, w, reverse=False, complement=False, activation="silu"):

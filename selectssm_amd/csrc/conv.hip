@@ -51,6 +51,7 @@ struct ConvArgs {
   int L, D, ntile;
   int ldx;  // row stride of x (dx is always (B,L,D))
   bool rev, comp;
+  bool acc;  // backward: dx += (SSM_ACCUMULATE)
   int act;
 };
 
@@ -167,6 +168,9 @@ __global__ void __launch_bounds__(kLanes* kCW) conv_bwd_kernel(ConvArgs<T> p) {
   }
   if (p.dx != nullptr && live) {
     T* __restrict__ dxb = p.dx + base;
+    // SSM_ACCUMULATE: the dx already there, loaded (like x and du) before any use
+    float dxo[kCT];
+    if (p.acc) load_rows<kCT>(dxo, dxb + q, t0, L, D, p.rev, true);
 #pragma unroll
     for (int i = 0; i < kCT; ++i) {
       const int t = t0 + i;
@@ -174,6 +178,10 @@ __global__ void __launch_bounds__(kLanes* kCW) conv_bwd_kernel(ConvArgs<T> p) {
         float g = 0.0f;
 #pragma unroll
         for (int k = 0; k < K; ++k) g = fmaf(wk[k], dv[i + K - 1 - k], g);
+        if (p.acc) {
+          pin(g);  // rounded on its own (with K = 1 the sum would fuse into the product)
+          g = dxo[i] + g;  // one rounding, as adding two dx arrays would
+        }
         const int r = p.rev ? L - 1 - t : t;
         st(dxb, (int64_t)r * D + q, g);
       }
@@ -256,7 +264,8 @@ int validate_conv(const ssm_conv_desc_t* desc, ConvShape* s) {
   if (desc->seqlen * desc->dim > (int64_t(1) << 31) - 1) return fail(SSM_ERR_INVALID, "seqlen*dim must be < 2^31");
   if (desc->ksize < 1 || desc->ksize > kMaxK) return fail(SSM_ERR_INVALID, "ksize must be in 1..8");
   if (desc->dtype != SSM_F32 && desc->dtype != SSM_BF16) return fail(SSM_ERR_INVALID, "dtype must be SSM_F32 or SSM_BF16");
-  if (desc->flags & ~(SSM_REVERSE | SSM_COMPLEMENT)) return fail(SSM_ERR_INVALID, "conv flags: only SSM_REVERSE, SSM_COMPLEMENT");
+  if (desc->flags & ~(SSM_REVERSE | SSM_COMPLEMENT | SSM_ACCUMULATE))
+    return fail(SSM_ERR_INVALID, "conv flags: only SSM_REVERSE, SSM_COMPLEMENT, SSM_ACCUMULATE");
   if (desc->activation != SSM_ACT_NONE && desc->activation != SSM_ACT_SILU && desc->activation != SSM_ACT_RELU)
     return fail(SSM_ERR_INVALID, "activation must be SSM_ACT_NONE, SSM_ACT_SILU or SSM_ACT_RELU");
   s->B = (int)desc->batch;
@@ -296,6 +305,7 @@ ConvArgs<T> conv_args(const ssm_conv_desc_t* desc, const ConvShape& s) {
   a.ldx = s.ldx;
   a.rev = (desc->flags & SSM_REVERSE) != 0;
   a.comp = (desc->flags & SSM_COMPLEMENT) != 0;
+  a.acc = (desc->flags & SSM_ACCUMULATE) != 0;
   a.act = desc->activation;
   return a;
 }

@@ -759,6 +759,8 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
   const bool srev = smap ? (p.flags & SSM_SKIP_REVERSE) != 0 : rev;
   const bool scomp = smap ? (p.flags & SSM_SKIP_COMPLEMENT) != 0 : comp;
   const bool gate = EPI && (p.flags & SSM_GATE);
+  // dz += the gate's gradient: the old dz at the output position is staged like z
+  const bool acc_dz = gate && (p.flags & SSM_ACCUMULATE);
   const bool skip = (p.flags & SSM_SKIP) != 0;  // non-EPI builds run only the skip from the scan position
   // u[t,d] is added (times D[d]) at the output position O(S(t,d)) with S the
   // skip source map: its gradient reads the gated dy there, which is the lane's
@@ -834,6 +836,7 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
   __shared__ float s_dB[kSB][kBwdWaves][kCK][NS], s_dC[kSB][kBwdWaves][kCK][NS];
   __shared__ float s_go[EB][ER][kBlkCh], s_gz[EB][ER][kBlkCh];  // gate: raw dy and z at the output position
   __shared__ float s_eu[EB][ER][kBlkCh], s_dyo[EB][ER][kBlkCh];
+  __shared__ float s_dza[EB][ER][kBlkCh];  // SSM_ACCUMULATE: dz before this call, at the output position
   __shared__ float s_ddt[kSB][kBwdWaves][kCK];  // broadcast delta: per-wave channel sums of ddelta
 
   const int dtD = p.dstride ? D : 1;
@@ -852,7 +855,7 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
 
   // fetch() only issues loads; commit() (after the block's compute) masks,
   // applies softplus and the gate and writes LDS
-  stg<T> r_u[RPT], r_dt[RPT], r_dy[RPT], r_gz[RPT], r_eu[RPT], r_dyo[RPT], r_zo[RPT];
+  stg<T> r_u[RPT], r_dt[RPT], r_dy[RPT], r_gz[RPT], r_eu[RPT], r_dyo[RPT], r_zo[RPT], r_dza[RPT];
   stg<T> r_B[BCE], r_C[BCE];
   float r_h[SPL];
   float h_next[SPL];  // checkpoint of the block staged by the last commit
@@ -896,6 +899,7 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
         const int prs = srev ? L - 1 - tc : tc;   // skip-source row
         const int prm = mrev ? L - 1 - tc : tc;   // row of O(S(.))
         if (gate) r_gz[k] = ld32r(z_b, (uint32_t)(pr * ldz + sq));
+        if (acc_dz) r_dza[k] = ld32r(dz_b, (uint32_t)(pr * D + sq));
         if (stage_eu) r_eu[k] = ld32r(u_b, (uint32_t)(prs * D + sqs));
         if (stage_dyo) {
           r_dyo[k] = ld32r(dy_b, (uint32_t)(prm * ldy + sqm));
@@ -920,6 +924,7 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
         const float gz = in ? val(r_gz[k]) : 0.0f;
         s_go[buf][i][scol] = go;
         s_gz[buf][i][scol] = gz;
+        if (acc_dz) s_dza[buf][i][scol] = in ? val(r_dza[k]) : 0.0f;
         dyg = go * gz * sigmoid(gz);
       }
       s_x[buf][i][scol] = in ? make_float4(val(r_u[k]), dtv, dyg, sg) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -1013,7 +1018,7 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
       float vCp[SPL], vBp[SPL];  // (SSM_BWD_PIPE) the previous step's products
       // gate: operands of the current 4-step group at this lane's output
       // step, read at the group's first step
-      float ge_u = 0.0f, ge_z = 0.0f, ge_o = 0.0f;
+      float ge_u = 0.0f, ge_z = 0.0f, ge_o = 0.0f, ge_a = 0.0f;
 #pragma unroll
       for (int i = 0; i < kCK; ++i) {
         if (i + PF < kCK) pre(i + PF, std::false_type{});
@@ -1022,6 +1027,7 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
           if (skip) ge_u = stage_eu ? s_eu[buf][ti][cw] : s_x[buf][ti][cw].x;
           ge_z = s_gz[buf][ti][cw];
           ge_o = s_go[buf][ti][cw];
+          if (acc_dz) ge_a = s_dza[buf][ti][cw];
         }
         __builtin_amdgcn_sched_barrier(0);
         const float uu = xr[i % R].x, dd = xr[i % R].y, dyv = xr[i % R].z;
@@ -1061,7 +1067,11 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
             if (skip) yv = fmaf(ge_u, Dq, yv);
             const float zz = ge_z;
             const float sg = sigmoid(zz);
-            const float dzv = ge_o * yv * sg * (1.0f + zz * (1.0f - sg));
+            float dzv = ge_o * yv * sg * (1.0f + zz * (1.0f - sg));
+            if (acc_dz) {
+              pin(dzv);  // rounded on its own, as a separate dz would be (no fused multiply-add)
+              dzv = ge_a + dzv;
+            }
             // both halves of the row hold the value; both store it
             if constexpr (kFull) {
               bst<T>(rdz, dzo, (uint32_t)(rev ? L - 1 - t0 - i : t0 + i - 3) * rowb, dzv);
@@ -1504,8 +1514,10 @@ int validate(const ssm_desc_t* desc, Shape* s) {
     return fail(SSM_ERR_INVALID, "checkpoints of one batch row must hold <= 2^30 floats");
   if (desc->dtype != SSM_F32 && desc->dtype != SSM_BF16) return fail(SSM_ERR_INVALID, "dtype must be SSM_F32 or SSM_BF16");
   if (desc->flags & ~(SSM_REVERSE | SSM_COMPLEMENT | SSM_SKIP | SSM_GATE | SSM_DELTA_SOFTPLUS | SSM_SKIP_MAP |
-                      SSM_SKIP_REVERSE | SSM_SKIP_COMPLEMENT))
+                      SSM_SKIP_REVERSE | SSM_SKIP_COMPLEMENT | SSM_ACCUMULATE))
     return fail(SSM_ERR_INVALID, "unknown flag bits");
+  if ((desc->flags & SSM_ACCUMULATE) && !(desc->flags & SSM_GATE))
+    return fail(SSM_ERR_INVALID, "SSM_ACCUMULATE (dz += ...) needs SSM_GATE");
   if ((desc->flags & (SSM_SKIP_REVERSE | SSM_SKIP_COMPLEMENT)) && !(desc->flags & SSM_SKIP_MAP))
     return fail(SSM_ERR_INVALID, "SSM_SKIP_REVERSE / SSM_SKIP_COMPLEMENT need SSM_SKIP_MAP");
   if (desc->delta_broadcast != 0 && desc->delta_broadcast != 1)
@@ -2011,7 +2023,8 @@ int ssm_bwd_pair(void* stream, const ssm_desc_t* desc, const ssm_bwd_io_t* io) {
     if (same) {
       if (s[0].nseg > 1)
         if (int rc = launch_bwd_agg<T>(st, s[0], a[0], a[1], 2 * s[0].B)) return rc;
-      if (SSM_PAIR_JOINT_BWD_MAIN) {
+      // a call accumulating into dz may share it with the other: run them in order
+      if (SSM_PAIR_JOINT_BWD_MAIN && !((desc[0].flags | desc[1].flags) & SSM_ACCUMULATE)) {
         if (int rc = launch_bwd_main<T>(st, &desc[0], s[0], a[0], a[1], 2 * s[0].B)) return rc;
       } else {
         for (int k = 0; k < 2; ++k)

@@ -31,7 +31,7 @@ from typing import Optional, Union
 import torch
 import torch.nn.functional as F
 
-from .conv import conv1d_act, conv1d_act_map
+from .conv import conv1d_act, conv1d_act_map, conv1d_act_pair
 from .scan import (_check_recursion, as_rows, bidirectional_selective_scan, needs_grad, resolve_chunking, scan_bwd,
                    scan_bwd_pair, scan_fwd, scan_fwd_pair, selective_scan)
 
@@ -359,7 +359,7 @@ class _PairCoreFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, uf, A_logf, Wbcf, bbcf, Wdtf, bdtf, Wpf, bpf, Df, zf,
-                ur, A_logr, Wbcr, bbcr, Wdtr, bdtr, Wpr, bpr, Dr, zr, N, rank, maps, want_ckpt):
+                ur, A_logr, Wbcr, bbcr, Wdtr, bdtr, Wpr, bpr, Dr, zr, N, rank, maps, want_ckpt, tied_z=False):
         B_, L_, E = uf.shape
         y = torch.empty(B_, L_, 2 * E, dtype=uf.dtype, device=uf.device)
         pf = _core_project(uf, A_logf, Wbcf, bbcf, Wdtf, bdtf, Wpf, bpf, N, rank)
@@ -374,6 +374,7 @@ class _PairCoreFn(torch.autograd.Function):
         sr = (ur, pr[0], Wbcr, Wdtr, Wpr, Dr, zr, pr[1], pr[2], pr[3], pr[4], ckr)
         ctx.save_for_backward(*sf, *sr)
         ctx.cfg = (N, rank, maps, len(sf))
+        ctx.tied_z = bool(tied_z) and zf is not None
         return y
 
     @staticmethod
@@ -385,10 +386,18 @@ class _PairCoreFn(torch.autograd.Function):
         sf, sr = saved[:k], saved[k:]
         (omf, smf), (omr, smr) = maps
         cf, cr = _scan_call(sf, omf[0], omf[1], N, smf), _scan_call(sr, omr[0], omr[1], N, smr)
-        scan_gf, scan_gr = scan_bwd_pair([dict(cf, ckpt=sf[-1], dy=dy[..., :E]), dict(cr, ckpt=sr[-1], dy=dy[..., E:])])
+        cf, cr = dict(cf, ckpt=sf[-1], dy=dy[..., :E]), dict(cr, ckpt=sr[-1], dy=dy[..., E:])
+        if ctx.tied_z:
+            # one z for both directions: the second scan adds its dz to the first's
+            z = sf[6]
+            cf["dz_out"] = torch.empty(z.shape, dtype=z.dtype, device=z.device)
+            cr["dz_out"], cr["dz_accumulate"] = cf["dz_out"], True
+        scan_gf, scan_gr = scan_bwd_pair([cf, cr])
         gf = _core_param_grads(sf, scan_gf, cf["dbc_out"], N, rank)
         gr = _core_param_grads(sr, scan_gr, cr["dbc_out"], N, rank)
-        return (*gf, *gr, None, None, None, None)
+        if ctx.tied_z:
+            gr = (*gr[:-1], None)  # zr is zf: its gradient is all in gf's dz
+        return (*gf, *gr, None, None, None, None, None)
 
 
 def _xor(a, b):
@@ -488,11 +497,13 @@ class SelectiveSSM(_FlaxModule):
         GF = _xor(conj, F)
         return GF, GF, F
 
-    def _prepare(self, x: torch.Tensor, projections: bool = True, conv_map=None) -> dict:
+    def _prepare(self, x: torch.Tensor, projections: bool = True, conv_map=None, conv_out=None) -> dict:
         """Everything of __call__ before the scan (selectssm.py:156-228): the scan's
         operands in the scan domain, with delta before its softplus (only the conv
         output u when ``projections`` is False).  ``conv_map``: the conv's (time,
-        channel) index map when not the module's own flip (a conjugation)."""
+        channel) index map when not the module's own flip (a conjugation).
+        ``conv_out``: the fused conv's output, already computed (for
+        :meth:`_conv_fused` modules only)."""
         if self.features is None:
             self._build(x.shape[-1], x.device)
         B, L, D = x.shape
@@ -510,9 +521,14 @@ class SelectiveSSM(_FlaxModule):
         if self.activation not in _FUSED_CONV_ACTS and self.activation != "gelu":
             raise Exception(f"Unknown activation: {self.activation}")
         coeffs = bool(diag) and "ssm_coeffs" in diag
-        fused = self.activation in _FUSED_CONV_ACTS and not coeffs
+        fused = self._conv_fused()
         cmap = self._flip() if conv_map is None else conv_map
-        u = conv1d_act_map(x, self.shift_conv.kernel, cmap[0], cmap[1], self.activation if fused else None)
+        if conv_out is not None:
+            if not fused:
+                raise ValueError("conv_out is the fused conv's output; this module runs its activation apart")
+            u = conv_out
+        else:
+            u = conv1d_act_map(x, self.shift_conv.kernel, cmap[0], cmap[1], self.activation if fused else None)
         if coeffs:
             self._sow("diagnostics", "conv_mean", u.mean())
             self._sow("diagnostics", "conv_sd", u.std(unbiased=False))
@@ -554,6 +570,11 @@ class SelectiveSSM(_FlaxModule):
         else:
             resolve_chunking(L, D, self.chunk_size, self.n_channel_groups)
         return dict(u=u, delta=dt, A=A, B=Bc, C=Cc, D=self.D)
+
+    def _conv_fused(self) -> bool:
+        """Whether the conv kernel applies the activation (no raw conv output sown)."""
+        d = self.diagnostics
+        return self.activation in _FUSED_CONV_ACTS and not (bool(d) and "ssm_coeffs" in d)
 
     def _unfused_outputs(self) -> bool:
         """Diagnostics that sow values the fused epilogue never materialises."""
@@ -850,11 +871,19 @@ class BidirectionalMamba(_FlaxModule):
                 x = bidirectional_selective_scan(pf, pr, complement=self.complement, delta_softplus=True)
             else:
                 mf, mr = f._maps(conj), r._maps(conj)
-                uf = f._prepare(xf, projections=False, conv_map=mf[0])["u"]
-                ur = r._prepare(xr, projections=False, conv_map=mr[0])["u"]
+                cf = cr = None
+                if xr is xf and f._conv_fused() and r._conv_fused():
+                    # tied in_proj block: both convs in one node, whose backward sums
+                    # their x-gradients inside the second conv kernel
+                    cf, cr = conv1d_act_pair(xf, f.shift_conv.kernel, r.shift_conv.kernel, mf[0], mr[0],
+                                             f.activation, r.activation)
+                uf = f._prepare(xf, projections=False, conv_map=mf[0], conv_out=cf)["u"]
+                ur = r._prepare(xr, projections=False, conv_map=mr[0], conv_out=cr)["u"]
                 io = uf.dtype
                 args = (*f._core_args(uf, as_rows(zf, io)[0]), *r._core_args(ur, as_rows(zr, io)[0]))
-                x = _PairCoreFn.apply(*args, f.hidden_features, f.rank, (mf[1:], mr[1:]), needs_grad(*args))
+                # tied gate: one z for both directions, whose dz the second scan backward adds to
+                x = _PairCoreFn.apply(*args, f.hidden_features, f.rank, (mf[1:], mr[1:]), needs_grad(*args),
+                                      zr is zf)
             f._finish(None)
             r._finish(None)
         elif rc:

@@ -231,13 +231,15 @@ def scan_fwd(u, delta, A, B, C, Dskip=None, z=None, reverse=False, complement=Fa
 
 
 def scan_bwd(u, delta, A, B, C, Dskip, z, ckpt, dy, reverse=False, complement=False, segments=0,
-             delta_softplus=False, dbc_out=None, skip_map=None):
+             delta_softplus=False, dbc_out=None, skip_map=None, dz_out=None, dz_accumulate=False):
     """Run ``ssm_bwd``.  Returns ``(du, ddelta, dA, dB, dC, dD, dz)`` (dD / dz None when unused);
     with ``delta_softplus``, ``ddelta`` is the gradient w.r.t. the pre-activation.
     ``dy`` and ``z`` may be row-strided column slices; dz is always contiguous.  When
     B and C are column slices of one array, dB and dC are the matching slices of
-    ``dbc_out`` (or of a new array of that width)."""
+    ``dbc_out`` (or of a new array of that width).  ``dz_out``: the dz array to
+    write, or with ``dz_accumulate`` to add the gate's gradient to (SSM_ACCUMULATE)."""
     flags = _flags(Dskip is not None, z is not None, reverse, complement, delta_softplus, skip_map)
+    flags |= _acc_flag(z, dz_out, dz_accumulate)
     ld_y, ld_z = row_stride(dy), (row_stride(z) if z is not None else 0)
     if ld_y is None or ld_z is None:
         raise ValueError("dy and z must be contiguous or column slices of a contiguous (B, L, W) tensor")
@@ -249,12 +251,30 @@ def scan_bwd(u, delta, A, B, C, Dskip, z, ckpt, dy, reverse=False, complement=Fa
     dA = torch.empty_like(A)
     dB, dC = _bc_grads(B, C, ld_bc, dbc_out)
     dD = torch.empty_like(Dskip) if Dskip is not None else None
-    dz = torch.empty_like(z) if z is not None else None
+    dz = _dz(z, dz_out)
     ws = _scratch(L.size_query(lib.ssm_bwd_workspace_bytes, desc), u.device)
     L.check(lib.ssm_bwd(_stream(), ctypes.byref(desc), _ptr(u), _ptr(delta), _ptr(A), _ptr(B), _ptr(C),
                         _ptr(Dskip), _ptr(z), _ptr(ckpt), _ptr(dy), _ptr(du), _ptr(ddelta), _ptr(dA),
                         _ptr(dB), _ptr(dC), _ptr(dD), _ptr(dz), _ptr(ws)))
     return du, ddelta, dA, dB, dC, dD, dz
+
+
+def _acc_flag(z, dz_out, accumulate):
+    if not accumulate:
+        return 0
+    if z is None or dz_out is None:
+        raise ValueError("dz_accumulate needs the gate (z) and the dz_out array to add to")
+    return L.SSM_ACCUMULATE
+
+
+def _dz(z, dz_out):
+    if z is None:
+        return None
+    if dz_out is None:
+        return torch.empty(z.shape, dtype=z.dtype, device=z.device)
+    if dz_out.shape != z.shape or dz_out.dtype != z.dtype or not dz_out.is_contiguous():
+        raise ValueError("dz_out must be a contiguous array of z's shape and dtype")
+    return dz_out
 
 
 def scan_fwd_pair(calls):
@@ -289,7 +309,8 @@ def scan_fwd_pair(calls):
 def scan_bwd_pair(calls):
     """Run ``ssm_bwd_pair``: two :func:`scan_bwd` calls, given as dicts of its
     keyword arguments (``u, delta, A, B, C, Dskip, z, ckpt, dy``, the flags and
-    optionally ``dbc_out``).
+    optionally ``dbc_out``, ``dz_out``, ``dz_accumulate``).  The second call may
+    accumulate into the first call's ``dz_out`` (BidirectionalMamba's tied gate).
     Returns the two ``(du, ddelta, dA, dB, dC, dD, dz)`` tuples."""
     if len(calls) != 2:
         raise ValueError("scan_bwd_pair takes two calls")
@@ -300,6 +321,7 @@ def scan_bwd_pair(calls):
         Dskip, z = c.get("Dskip"), c.get("z")
         flags = _flags(Dskip is not None, z is not None, c.get("reverse", False), c.get("complement", False),
                        c.get("delta_softplus", False), c.get("skip_map"))
+        flags |= _acc_flag(z, c.get("dz_out"), c.get("dz_accumulate", False))
         ld_y, ld_z = row_stride(dy), (row_stride(z) if z is not None else 0)
         if ld_y is None or ld_z is None:
             raise ValueError("dy and z must be contiguous or column slices of a contiguous (B, L, W) tensor")
@@ -307,7 +329,7 @@ def scan_bwd_pair(calls):
         descs[k] = _desc(u, delta, A, flags, c.get("segments", 0), ld_y=ld_y, ld_z=ld_z, ld_bc=ld_bc)
         g = (torch.empty_like(u), torch.empty_like(delta), torch.empty_like(A),
              *_bc_grads(B, C, ld_bc, c.get("dbc_out")), torch.empty_like(Dskip) if Dskip is not None else None,
-             torch.empty_like(z) if z is not None else None)
+             _dz(z, c.get("dz_out")))
         ws = _scratch(L.size_query(lib.ssm_bwd_workspace_bytes, descs[k]), u.device)
         ios[k] = L.SsmBwdIo(_ptr(u), _ptr(delta), _ptr(A), _ptr(B), _ptr(C), _ptr(Dskip), _ptr(z), _ptr(c["ckpt"]),
                             _ptr(dy), *(_ptr(t) for t in g), _ptr(ws))

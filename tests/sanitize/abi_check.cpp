@@ -77,7 +77,8 @@ static void invalid_descs() {
       {"dstate 33", [](ssm_desc_t& d) { d.dstate = 33; }},
       {"dtype 9", [](ssm_desc_t& d) { d.dtype = 9; }},
       {"skip-map bits without SSM_SKIP_MAP", [](ssm_desc_t& d) { d.flags = SSM_SKIP_REVERSE; }},
-      {"flags 256", [](ssm_desc_t& d) { d.flags = 256; }},
+      {"flags 512", [](ssm_desc_t& d) { d.flags = 512; }},
+      {"SSM_ACCUMULATE without SSM_GATE", [](ssm_desc_t& d) { d.flags = SSM_ACCUMULATE; }},
       {"delta_broadcast 2", [](ssm_desc_t& d) { d.delta_broadcast = 2; }},
       {"segments 1025", [](ssm_desc_t& d) { d.segments = 1025; }},
       {"ld_y < dim", [](ssm_desc_t& d) { d.ld_y = 3; }},

@@ -33,7 +33,7 @@ def test_header_constants_match_binding():
     consts = dict(re.findall(r"#define (SSM_\w+) (\d+)u?", text))
     for k in ("SSM_OK", "SSM_ERR_INVALID", "SSM_ERR_UNSUPPORTED", "SSM_ERR_HIP", "SSM_F32", "SSM_BF16",
               "SSM_REVERSE", "SSM_COMPLEMENT", "SSM_SKIP", "SSM_GATE", "SSM_DELTA_SOFTPLUS", "SSM_SKIP_MAP",
-              "SSM_SKIP_REVERSE", "SSM_SKIP_COMPLEMENT",
+              "SSM_SKIP_REVERSE", "SSM_SKIP_COMPLEMENT", "SSM_ACCUMULATE",
               "SSM_ACT_NONE", "SSM_ACT_SILU", "SSM_ACT_RELU"):
         assert int(consts[k]) == getattr(L, k), k
     assert int(consts["SSM_ABI_VERSION"]) == L.ABI_VERSION
@@ -90,7 +90,8 @@ def test_split_forward_needs_its_workspace():
 
 @pytest.mark.parametrize("field,value,msg", [
     ("batch", 0, b"batch, seqlen and dim"), ("dstate", 0, b"dstate"), ("dtype", 7, b"dtype"),
-    ("flags", 256, b"unknown flag"), ("flags", 64, b"SKIP_MAP"), ("flags", 128, b"SKIP_MAP"),
+    ("flags", 512, b"unknown flag"), ("flags", 64, b"SKIP_MAP"), ("flags", 128, b"SKIP_MAP"),
+    ("flags", 256, b"needs SSM_GATE"),
     ("delta_broadcast", 3, b"delta_broadcast"),
     ("segments", -1, b"segments"), ("segments", 1025, b"segments"), ("ld_y", 63, b"ld_y"), ("ld_z", 1, b"ld_z"),
     ("ld_y", 1 << 28, b"seqlen*ld_y"), ("ld_bc", 15, b"ld_bc"), ("ld_bc", 1 << 28, b"ld_bc"),

@@ -185,6 +185,10 @@ MAMBA_CASES = [
     dict(concatenate_fwd_rev=False, norm_type="layer"),
     dict(activation="gelu", mlp_layer=True),
     dict(activation="relu", tie_gate=True, ssm_args=dict(shift_conv_size=4, custom_vjp_scan=True)),
+    # one tie at a time on the fused pair path: the x-gradient summed in the second
+    # conv kernel, or the dz summed in the second scan kernel
+    dict(tie_in_proj=True),
+    dict(complement=True, tie_gate=True),
 ]
 
 
