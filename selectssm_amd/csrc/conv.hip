@@ -137,7 +137,9 @@ __global__ void __launch_bounds__(kLanes* kCW) conv_fwd_kernel(ConvArgs<T> p) {
   }
 }
 
-template <int K, typename T>
+// ACC: dx += (SSM_ACCUMULATE), a separate build so that the plain backward's
+// loads and registers are those of a kernel without the extra dx read
+template <int K, bool ACC, typename T>
 __global__ void __launch_bounds__(kLanes* kCW) conv_bwd_kernel(ConvArgs<T> p) {
   const int lane = threadIdx.x & (kLanes - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
@@ -169,8 +171,8 @@ __global__ void __launch_bounds__(kLanes* kCW) conv_bwd_kernel(ConvArgs<T> p) {
   if (p.dx != nullptr && live) {
     T* __restrict__ dxb = p.dx + base;
     // SSM_ACCUMULATE: the dx already there, loaded (like x and du) before any use
-    float dxo[kCT];
-    if (p.acc) load_rows<kCT>(dxo, dxb + q, t0, L, D, p.rev, true);
+    float dxo[ACC ? kCT : 1];
+    if constexpr (ACC) load_rows<kCT>(dxo, dxb + q, t0, L, D, p.rev, true);
 #pragma unroll
     for (int i = 0; i < kCT; ++i) {
       const int t = t0 + i;
@@ -178,7 +180,7 @@ __global__ void __launch_bounds__(kLanes* kCW) conv_bwd_kernel(ConvArgs<T> p) {
         float g = 0.0f;
 #pragma unroll
         for (int k = 0; k < K; ++k) g = fmaf(wk[k], dv[i + K - 1 - k], g);
-        if (p.acc) {
+        if constexpr (ACC) {
           pin(g);  // rounded on its own (with K = 1 the sum would fuse into the product)
           g = dxo[i] + g;  // one rounding, as adding two dx arrays would
         }
@@ -337,7 +339,10 @@ int launch_conv_bwd(hipStream_t st, const ssm_conv_desc_t* desc, const ConvShape
   const dim3 grid((s.D + kLanes - 1) / kLanes, s.ntile, s.B);
   dispatch_k(s.K, [&](auto kc) {
     constexpr int K = decltype(kc)::value;
-    hipLaunchKernelGGL((conv_bwd_kernel<K, T>), grid, dim3(kLanes * kCW), 0, st, a);
+    if (a.acc)
+      hipLaunchKernelGGL((conv_bwd_kernel<K, true, T>), grid, dim3(kLanes * kCW), 0, st, a);
+    else
+      hipLaunchKernelGGL((conv_bwd_kernel<K, false, T>), grid, dim3(kLanes * kCW), 0, st, a);
   });
   if (int rc = hip_check(hipGetLastError(), "ssm_conv_bwd launch")) return rc;
   if (dw != nullptr) {

@@ -720,10 +720,13 @@ struct BwdStage {
 // hand over (ssm_bwd_agg_kernel), and writes du, ddelta, dz and the partial
 // sums of dB, dC, dA, dD (and of a broadcast ddelta).
 // SPL: states per lane (N <= 8 * SPL).  EPI: the gate and the reverse skip.
-// BC: delta is (B,L,1), shared by the channels.
+// BC: delta is (B,L,1), shared by the channels.  ACC (with EPI): dz += the
+// gate's gradient (SSM_ACCUMULATE), a build of its own so that the plain
+// gated backward keeps its registers.
 // Rows of p0 below rows0, rows of p1 above, as ssm_fwd_kernel.
-template <int SPL, bool EPI, bool BC, typename T>
+template <int SPL, bool EPI, bool BC, bool ACC, typename T>
 __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T> p0, BwdArgs<T> p1, int rows0) {
+  static_assert(EPI || !ACC, "dz is accumulated only by the gated (EPI) builds");
   const bool second = (int)blockIdx.y >= rows0;
   const BwdArgs<T> p = pick_args<T>(p0, p1, second);
   constexpr int NS = 8 * SPL;
@@ -760,7 +763,7 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
   const bool scomp = smap ? (p.flags & SSM_SKIP_COMPLEMENT) != 0 : comp;
   const bool gate = EPI && (p.flags & SSM_GATE);
   // dz += the gate's gradient: the old dz at the output position is staged like z
-  const bool acc_dz = gate && (p.flags & SSM_ACCUMULATE);
+  const bool acc_dz = ACC && gate;
   const bool skip = (p.flags & SSM_SKIP) != 0;  // non-EPI builds run only the skip from the scan position
   // u[t,d] is added (times D[d]) at the output position O(S(t,d)) with S the
   // skip source map: its gradient reads the gated dy there, which is the lane's
@@ -1744,12 +1747,17 @@ int launch_bwd_main(hipStream_t st, const ssm_desc_t* desc, const Shape& s, cons
   if (!dispatch_spl<2, 4>(s.spl_b, s.epi, [&](auto spl, auto epi) {
         constexpr int S = decltype(spl)::value;
         constexpr bool E = decltype(epi)::value;
-        if (desc->delta_broadcast)
-          hipLaunchKernelGGL((ssm_bwd_kernel<S, E, true, T>), dim3(s.ncb, rows, s.nseg), dim3(kWave * kBwdWaves), 0,
-                             st, a0, a1, s.B);
-        else
-          hipLaunchKernelGGL((ssm_bwd_kernel<S, E, false, T>), dim3(s.ncb, rows, s.nseg), dim3(kWave * kBwdWaves), 0,
-                             st, a0, a1, s.B);
+        auto go = [&](auto bc, auto acc) {
+          constexpr bool kBC = decltype(bc)::value, kAcc = E && decltype(acc)::value;
+          hipLaunchKernelGGL((ssm_bwd_kernel<S, E, kBC, kAcc, T>), dim3(s.ncb, rows, s.nseg),
+                             dim3(kWave * kBwdWaves), 0, st, a0, a1, s.B);
+        };
+        const bool acc = (desc->flags & SSM_ACCUMULATE) != 0;  // validated: only with the gate (EPI)
+        if (desc->delta_broadcast) {
+          if (acc) go(std::true_type{}, std::true_type{}); else go(std::true_type{}, std::false_type{});
+        } else {
+          if (acc) go(std::false_type{}, std::true_type{}); else go(std::false_type{}, std::false_type{});
+        }
       }))
     return fail(SSM_ERR_UNSUPPORTED, "no kernel variant for this shape");
   return hip_check(hipGetLastError(), "ssm_bwd launch");
