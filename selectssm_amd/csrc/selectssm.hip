@@ -987,8 +987,13 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
 #pragma unroll
     for (int j = 0; j < SPL; ++j) dAblk[j] = 0.0f;
     float dDblk = 0.0f;
-    auto sweeps = [&](auto full_tag) {
+    // the gate is a compile-time property of each instance of the sweeps
+    // (branches in the unrolled step loop would split it into many small
+    // scheduling regions)
+    auto sweeps = [&](auto full_tag, auto gate_tag) {
       constexpr bool kFull = decltype(full_tag)::value;
+      constexpr bool kGate = EPI && decltype(gate_tag)::value;
+      constexpr bool kAccDz = ACC && kGate;
       float a_s[kCK][SPL], hp_s[kCK][SPL];
       // (u, delta, dy) and B of the block kept in registers from the
       // recompute for the adjoint where they fit (2 states per lane): the
@@ -1025,12 +1030,12 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
 #pragma unroll
       for (int i = 0; i < kCK; ++i) {
         if (i + PF < kCK) pre(i + PF, std::false_type{});
-        if (gate && (i & 3) == 0) {
+        if (kGate && (i & 3) == 0) {
           const int ti = i + yrow_step(orow);
           if (skip) ge_u = stage_eu ? s_eu[buf][ti][cw] : s_x[buf][ti][cw].x;
           ge_z = s_gz[buf][ti][cw];
           ge_o = s_go[buf][ti][cw];
-          if (acc_dz) ge_a = s_dza[buf][ti][cw];
+          if constexpr (kAccDz) ge_a = s_dza[buf][ti][cw];
         }
         __builtin_amdgcn_sched_barrier(0);
         const float uu = xr[i % R].x, dd = xr[i % R].y, dyv = xr[i % R].z;
@@ -1057,7 +1062,7 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
         } else {
           s_dC[sb][wave][i][SPL * g + sig] = chan_reduce8<SPL>(vC);
         }
-        if (gate) {
+        if constexpr (kGate) {
           float ys = bc[i % R][SPL] * h[0];
 #pragma unroll
           for (int j = 1; j < SPL; ++j) ys = fmaf(bc[i % R][SPL + j], h[j], ys);
@@ -1071,7 +1076,7 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
             const float zz = ge_z;
             const float sg = sigmoid(zz);
             float dzv = ge_o * yv * sg * (1.0f + zz * (1.0f - sg));
-            if (acc_dz) {
+            if constexpr (kAccDz) {
               pin(dzv);  // rounded on its own, as a separate dz would be (no fused multiply-add)
               dzv = ge_a + dzv;
             }
@@ -1158,7 +1163,15 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
         }
       }
     };
-    if (full) sweeps(std::true_type{}); else sweeps(std::false_type{});
+    if constexpr (EPI) {
+      if (gate) {
+        if (full) sweeps(std::true_type{}, std::true_type{}); else sweeps(std::false_type{}, std::true_type{});
+      } else {
+        if (full) sweeps(std::true_type{}, std::false_type{}); else sweeps(std::false_type{}, std::false_type{});
+      }
+    } else {
+      if (full) sweeps(std::true_type{}, std::false_type{}); else sweeps(std::false_type{}, std::false_type{});
+    }
 #pragma unroll
     for (int j = 0; j < SPL; ++j) dAmid[j] += dAblk[j];
     dDmid += dDblk;
