@@ -987,12 +987,13 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
 #pragma unroll
     for (int j = 0; j < SPL; ++j) dAblk[j] = 0.0f;
     float dDblk = 0.0f;
-    // the gate is a compile-time property of each instance of the sweeps
-    // (branches in the unrolled step loop would split it into many small
-    // scheduling regions)
-    auto sweeps = [&](auto full_tag, auto gate_tag) {
+    // the gate and the skip / softplus terms are compile-time properties of
+    // each instance of the sweeps (branches in the unrolled step loop would
+    // split it into many small scheduling regions)
+    auto sweeps = [&](auto full_tag, auto gate_tag, auto sd_tag) {
       constexpr bool kFull = decltype(full_tag)::value;
       constexpr bool kGate = EPI && decltype(gate_tag)::value;
+      constexpr bool kSD = decltype(sd_tag)::value;  // skip || dsp
       constexpr bool kAccDz = ACC && kGate;
       float a_s[kCK][SPL], hp_s[kCK][SPL];
       // (u, delta, dy) and B of the block kept in registers from the
@@ -1134,7 +1135,7 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
           val += dpp_mov<kDppRor8>(val);
           const int ti = i + ((orow & 1) ? 0 : 1);
           const int t = t0 + ti;
-          if (skip || dsp) {
+          if constexpr (kSD) {
             // du[t,d] += D[d] dy_out[t,d] and dD[d] += dy_out[t,d] u[t,d] on
             // du rows (Ddu is 0 without the skip); ddelta through softplus
             // (x.w is softplus'(delta), or 1)
@@ -1163,14 +1164,16 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
         }
       }
     };
+    auto run_sweeps = [&](auto gate_tag, auto sd_tag) {
+      if (full) sweeps(std::true_type{}, gate_tag, sd_tag); else sweeps(std::false_type{}, gate_tag, sd_tag);
+    };
+    auto run_sd = [&](auto gate_tag) {
+      if (skip || dsp) run_sweeps(gate_tag, std::true_type{}); else run_sweeps(gate_tag, std::false_type{});
+    };
     if constexpr (EPI) {
-      if (gate) {
-        if (full) sweeps(std::true_type{}, std::true_type{}); else sweeps(std::false_type{}, std::true_type{});
-      } else {
-        if (full) sweeps(std::true_type{}, std::false_type{}); else sweeps(std::false_type{}, std::false_type{});
-      }
+      if (gate) run_sd(std::true_type{}); else run_sd(std::false_type{});
     } else {
-      if (full) sweeps(std::true_type{}, std::false_type{}); else sweeps(std::false_type{}, std::false_type{});
+      run_sd(std::false_type{});
     }
 #pragma unroll
     for (int j = 0; j < SPL; ++j) dAmid[j] += dAblk[j];
