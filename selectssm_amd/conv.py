@@ -108,7 +108,7 @@ class ConvActPairFn(torch.autograd.Function):
         dx = None
         dw = []
         for du, w, cfg, need_dw in ((du1, w1, cfg1, ctx.needs_input_grad[1]), (du2, w2, cfg2, ctx.needs_input_grad[2])):
-            if du is None:
+            if du is None or not (need_dx or need_dw):
                 dw.append(None)
                 continue
             d, g = conv_bwd(x, w, du.to(x.dtype).contiguous(), *cfg, need_dx=need_dx, need_dw=need_dw, dx_out=dx,

@@ -111,3 +111,29 @@ def test_conv_dx_accumulates_and_pair_node(dtype, maps):
         tol = 2e-2 * float(ref.abs().max())
         assert torch.allclose(acc.float(), ref, rtol=2e-2, atol=tol)
         assert torch.equal(xx.grad, acc)
+
+
+def test_conv_pair_node_partial_gradients():
+    """The pair node when only some inputs need a gradient: x alone, or one kernel alone."""
+    from selectssm_amd.conv import conv1d_act_map, conv1d_act_pair
+
+    gen = torch.Generator(device="cuda").manual_seed(44)
+    x = torch.randn(1, 200, 64, device="cuda", generator=gen)
+    w1 = torch.randn(3, 64, device="cuda", generator=gen)
+    w2 = torch.randn(3, 64, device="cuda", generator=gen)
+    du = torch.randn(x.shape, device="cuda", generator=gen)
+    maps = ((False, False), (True, True))
+    # only w2 needs a gradient: the first conv's backward is skipped
+    p2 = w2.clone().requires_grad_(True)
+    u1, u2 = conv1d_act_pair(x, w1, p2, *maps)
+    (u1 * du).sum().add((u2 * du).sum()).backward()
+    q2 = w2.clone().requires_grad_(True)
+    (conv1d_act_map(x, q2, *maps[1]) * du).sum().backward()
+    assert torch.equal(p2.grad, q2.grad)
+    # only x needs a gradient, and only the second output is used
+    xx = x.clone().requires_grad_(True)
+    _, u2 = conv1d_act_pair(xx, w1, w2, *maps)
+    (u2 * du).sum().backward()
+    xr = x.clone().requires_grad_(True)
+    (conv1d_act_map(xr, w2, *maps[1]) * du).sum().backward()
+    assert torch.equal(xx.grad, xr.grad)
