@@ -35,10 +35,12 @@
 //
 // Time is walked in tiles staged in LDS: the next tile's global loads are
 // issued before the current tile computes and written to the other buffer
-// after it; inside a tile the LDS operands of step i + PF are read while step
-// i computes (sched_barrier keeps the reads where they are written).  Staged
-// bf16 values stay raw 16-bit registers until they are written to LDS (a
-// widening next to the load would wait for it there).  With 2 states per lane
+// after it (the backward: between the block's two sweeps, when none of the
+// block's stores is in flight yet); inside a tile the LDS operands of step
+// i + PF are read while step i computes (sched_barrier keeps the reads where
+// they are written).  Staged bf16 values stay raw 16-bit registers until they
+// are written to LDS (a widening next to the load would wait for it there).
+// With 2 states per lane
 // the backward keeps the block's (u, delta, dy) and B in registers from its
 // recompute sweep, so the adjoint sweep reads only C from LDS.  Sums
 // over channel blocks (dB, dC, broadcast ddelta) and over rows / segments
@@ -836,6 +838,10 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
   // sweeps write the other set
   constexpr int kSB = (SPL == 4 && EPI) ? 1 : 2;
   int sb = 0;
+  // the next block's staging commit runs between the block's two sweeps,
+  // except in the builds whose registers it would push into spills (the
+  // accumulating gated one and the gated N > 16 ones), where it follows them
+  constexpr bool kMidCommit = !ACC && !(SPL == 4 && EPI);
   __shared__ float s_dB[kSB][kBwdWaves][kCK][NS], s_dC[kSB][kBwdWaves][kCK][NS];
   __shared__ float s_go[EB][ER][kBlkCh], s_gz[EB][ER][kBlkCh];  // gate: raw dy and z at the output position
   __shared__ float s_eu[EB][ER][kBlkCh], s_dyo[EB][ER][kBlkCh];
@@ -856,8 +862,8 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
   T* __restrict__ out_b = (is_du ? p.du : p.ddelta) + (int64_t)b * L * D;  // ddelta only when (B,L,D)
   T* __restrict__ dz_b = EPI ? p.dz + (int64_t)b * L * D : nullptr;
 
-  // fetch() only issues loads; commit() (after the block's compute) masks,
-  // applies softplus and the gate and writes LDS
+  // fetch() only issues loads; commit() (between the block's sweeps, or after
+  // them, kMidCommit) masks, applies softplus and the gate and writes LDS
   stg<T> r_u[RPT], r_dt[RPT], r_dy[RPT], r_gz[RPT], r_eu[RPT], r_dyo[RPT], r_zo[RPT], r_dza[RPT];
   stg<T> r_B[BCE], r_C[BCE];
   float r_h[SPL];
@@ -1090,6 +1096,14 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
           }
         }
       }
+      // The next block's operands go to LDS here, between the sweeps (that
+      // buffer was last read before the previous block-end barrier).  One
+      // counter (vmcnt) covers both loads and stores, and the wait for this
+      // block's fetch loads is vmcnt(0): after the adjoint it also waited for
+      // the adjoint's last du / ddelta stores, here none is in flight.
+      if constexpr (kMidCommit) {
+        if (more) commit(buf ^ 1, blk - 1);
+      }
       // adjoint, backwards through the block
       float v1p = 0.0f, v2p = 0.0f;
 #pragma unroll
@@ -1209,14 +1223,18 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
     }
     };
     if constexpr (kSB == 2) {
-      if (more) commit(buf ^ 1, blk - 1);
+      if constexpr (!kMidCommit) {
+        if (more) commit(buf ^ 1, blk - 1);
+      }
       __syncthreads();
       totals();
       sb ^= 1;
     } else {
       __syncthreads();
       totals();
-      if (more) commit(buf ^ 1, blk - 1);
+      if constexpr (!kMidCommit) {
+        if (more) commit(buf ^ 1, blk - 1);
+      }
       __syncthreads();
     }
   }
