@@ -511,10 +511,11 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
 // segments seg < nseg - 1, writes the segment's state at its end from a zero
 // start, H = sum_t P_t B_t delta_t u_t with P_t the product of the decays
 // after step t, and the whole segment's decay product P.  It walks the segment
-// from its end (H += P B delta u, then P *= a), so once every P of the
-// workgroup is 0 (flushed at tile ends, flush_tiny) all earlier steps add
-// exact zeros and the walk stops there: with decaying states only the last
-// few thousand steps of a long segment are read.
+// from its end a tile at a time (P: the product of the decays after the tile;
+// H += P times the tile's own sum, then P *= the tile's decay), so once every
+// P of the workgroup is 0 (flushed at tile ends, flush_tiny) all earlier
+// steps add exact zeros and the walk stops there: with decaying states only
+// the last few thousand steps of a long segment are read.
 template <int SPL, bool SP, typename T>
 __device__ __forceinline__ void fwd_agg_body(const FwdArgs<T>& p, const int b) {
   constexpr int NS = 4 * SPL;
@@ -619,6 +620,13 @@ __device__ __forceinline__ void fwd_agg_body(const FwdArgs<T>& p, const int b) {
     };
 #pragma unroll
     for (int k = 0; k < PF; ++k) pre(kTT - 1 - k);
+    // the tile's terms relative to its end: Ht = sum_i e_i B_i delta_i u_i
+    // with e_i = exp2(A log2(e) s_i), s_i the sum of the tile's deltas after
+    // step i; then H += P Ht and P *= exp2(A log2(e) s) once per tile.  One
+    // exponential per state and step as before, and no running product.
+    float Ht[SPL], s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) Ht[j] = 0.0f;
 #pragma unroll
     for (int i = kTT - 1; i >= 0; --i) {
       if (i - PF >= 0) pre(i - PF);
@@ -626,15 +634,15 @@ __device__ __forceinline__ void fwd_agg_body(const FwdArgs<T>& p, const int b) {
       const float uu = ud[i % R].x, dd = ud[i % R].y;
       const float w = dd * uu;
 #pragma unroll
-      for (int j = 0; j < SPL; ++j) {
-        H[j] = fmaf(P[j], Bq[i % R][j] * w, H[j]);
-        P[j] *= fast_exp2(A2[j] * dd);
-      }
+      for (int j = 0; j < SPL; ++j) Ht[j] = fmaf(fast_exp2(A2[j] * s), Bq[i % R][j] * w, Ht[j]);
+      s += dd;
 #pragma unroll
-      for (int j = 0; j < SPL; ++j) {
-        pin(H[j]);
-        pin(P[j]);
-      }
+      for (int j = 0; j < SPL; ++j) pin(Ht[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) {
+      H[j] = fmaf(P[j], Ht[j], H[j]);
+      P[j] *= fast_exp2(A2[j] * s);
     }
     if (more) commit(buf ^ 1, t0 - kTT);
     // products below the smallest normal float are flushed to zero; every
@@ -1263,9 +1271,11 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
 // (f_t = C_t dy_t + a_{t+1} f_{t+1}, ssmrecscan.py:96-100, 150-153), i.e.
 // G = sum_t P_t C_t dy_t with P_t the product of the decays up to and including
 // step t, and the whole segment's decay product P, through which a carry from
-// the right enters G.  It walks the segment forwards (P *= a, then G += P C dy),
-// so once every P of the workgroup is 0 (flushed at tile ends, flush_tiny) all
-// later steps add exact zeros and the walk stops there.
+// the right enters G.  It walks the segment forwards a tile at a time (P: the
+// product of the decays before the tile; G += P times the tile's own sum, then
+// P *= the tile's decay), so once every P of the workgroup is 0 (flushed at
+// tile ends, flush_tiny) all later steps add exact zeros and the walk stops
+// there.
 template <int SPL, bool EPI, typename T>
 __device__ __forceinline__ void bwd_agg_body(const BwdArgs<T>& p, const int b) {
   constexpr int NS = 8 * SPL;
@@ -1386,21 +1396,27 @@ __device__ __forceinline__ void bwd_agg_body(const BwdArgs<T>& p, const int b) {
     };
 #pragma unroll
     for (int i = 0; i < PF; ++i) pre(i);
+    // the tile's terms relative to its start: Gt = sum_i e_i C_i dy_i with
+    // e_i = exp2(A log2(e) s_i), s_i the sum of the tile's deltas up to and
+    // including step i; then G += P Gt and P *= exp2(A log2(e) s) once per tile
+    float Gt[SPL], s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) Gt[j] = 0.0f;
 #pragma unroll
     for (int i = 0; i < kTT; ++i) {
       if (i + PF < kTT) pre(i + PF);
       __builtin_amdgcn_sched_barrier(0);
       const float dd = xd[i % R].x, dyv = xd[i % R].y;
+      s += dd;
 #pragma unroll
-      for (int j = 0; j < SPL; ++j) {
-        P[j] *= fast_exp2(A2[j] * dd);
-        G[j] = fmaf(P[j], Cq[i % R][j] * dyv, G[j]);
-      }
+      for (int j = 0; j < SPL; ++j) Gt[j] = fmaf(fast_exp2(A2[j] * s), Cq[i % R][j] * dyv, Gt[j]);
 #pragma unroll
-      for (int j = 0; j < SPL; ++j) {
-        pin(G[j]);
-        pin(P[j]);
-      }
+      for (int j = 0; j < SPL; ++j) pin(Gt[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) {
+      G[j] = fmaf(P[j], Gt[j], G[j]);
+      P[j] *= fast_exp2(A2[j] * s);
     }
     if (more) commit(buf ^ 1, t0 + kTT);
     // as in the forward aggregate: flushed products end the walk
