@@ -850,6 +850,10 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
   // except in the builds whose registers it would push into spills (the
   // accumulating gated one and the gated N > 16 ones), where it follows them
   constexpr bool kMidCommit = !ACC && !(SPL == 4 && EPI);
+  // with two sets and the commit between the sweeps, a block's dB / dC totals
+  // are added in the next block, after its commit, instead of right after the
+  // block-end barrier, where every wave waited on the same LDS reads at once
+  constexpr bool kLateTotals = kSB == 2 && kMidCommit;
   __shared__ float s_dB[kSB][kBwdWaves][kCK][NS], s_dC[kSB][kBwdWaves][kCK][NS];
   __shared__ float s_go[EB][ER][kBlkCh], s_gz[EB][ER][kBlkCh];  // gate: raw dy and z at the output position
   __shared__ float s_eu[EB][ER][kBlkCh], s_dyo[EB][ER][kBlkCh];
@@ -983,6 +987,29 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
     }
   };
 
+  // dB, dC totals of the block at t0x of this channel block, from LDS set sbx:
+  // the 8 waves' sums added in order
+  auto totals = [&](int t0x, int sbx) {
+    for (int e = tid; e < 2 * kCK * NS; e += NT) {
+      const int which = e / (kCK * NS);
+      const int r = e - which * (kCK * NS);
+      const int i = r / NS, n = r - (r / NS) * NS;
+      if (n < N && t0x + i < L) {
+        float s = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kBwdWaves; ++w) s += which ? s_dC[sbx][w][i][n] : s_dB[sbx][w][i][n];
+        float* dst = which ? p.ws_dC : p.ws_dB;
+        dst[(((int64_t)cb * p.Bt + b) * L + t0x + i) * N + n] = s;
+      }
+    }
+    if (BC && tid < kCK && t0x + tid < L) {
+      float s = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kBwdWaves; ++w) s += s_ddt[sbx][w][tid];
+      p.ws_ddt[((int64_t)cb * p.Bt + b) * L + t0x + tid] = s;
+    }
+  };
+
   fetch(blk_hi - 1);
   commit(0, blk_hi - 1);
   __syncthreads();
@@ -1112,6 +1139,12 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
       if constexpr (kMidCommit) {
         if (more) commit(buf ^ 1, blk - 1);
       }
+      // the previous block's dB / dC totals (its sums are in the other set,
+      // complete since the last barrier; that set is written again only after
+      // the next one)
+      if constexpr (kLateTotals) {
+        if (blk < blk_hi - 1) totals(t0 + kCK, sb ^ 1);
+      }
       // adjoint, backwards through the block
       float v1p = 0.0f, v2p = 0.0f;
 #pragma unroll
@@ -1209,43 +1242,26 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
       dDacc += dDmid;
       dDmid = 0.0f;
     }
-    // dB, dC totals of this channel block: the 8 waves' sums added in order
-    auto totals = [&]() {
-    for (int e = tid; e < 2 * kCK * NS; e += NT) {
-      const int which = e / (kCK * NS);
-      const int r = e - which * (kCK * NS);
-      const int i = r / NS, n = r - (r / NS) * NS;
-      if (n < N && t0 + i < L) {
-        float s = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kBwdWaves; ++w) s += which ? s_dC[sb][w][i][n] : s_dB[sb][w][i][n];
-        float* dst = which ? p.ws_dC : p.ws_dB;
-        dst[(((int64_t)cb * p.Bt + b) * L + t0 + i) * N + n] = s;
-      }
-    }
-    if (BC && tid < kCK && t0 + tid < L) {
-      float s = 0.0f;
-#pragma unroll
-      for (int w = 0; w < kBwdWaves; ++w) s += s_ddt[sb][w][tid];
-      p.ws_ddt[((int64_t)cb * p.Bt + b) * L + t0 + tid] = s;
-    }
-    };
-    if constexpr (kSB == 2) {
+    if constexpr (kLateTotals) {
+      __syncthreads();
+      sb ^= 1;
+    } else if constexpr (kSB == 2) {
       if constexpr (!kMidCommit) {
         if (more) commit(buf ^ 1, blk - 1);
       }
       __syncthreads();
-      totals();
+      totals(t0, sb);
       sb ^= 1;
     } else {
       __syncthreads();
-      totals();
+      totals(t0, sb);
       if constexpr (!kMidCommit) {
         if (more) commit(buf ^ 1, blk - 1);
       }
       __syncthreads();
     }
   }
+  if constexpr (kLateTotals) totals(blk_lo * kCK, sb ^ 1);  // the last block's, after its barrier
 
 #pragma unroll
   for (int j = 0; j < SPL; ++j)
