@@ -842,8 +842,8 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
   __shared__ __attribute__((aligned(16))) float s_bc[2][kCK][8][SPL][2 * SPL];
   // per-wave channel sums, in two sets where LDS allows (all but N > 16 with
   // the gate): a block's totals are then added after the one barrier that
-  // also publishes the next block's staged operands, while the next block's
-  // sweeps write the other set
+  // also publishes the next block's staged operands (in the next block, with
+  // kLateTotals), while the next block's sweeps write the other set
   constexpr int kSB = (SPL == 4 && EPI) ? 1 : 2;
   int sb = 0;
   // the next block's staging commit runs between the block's two sweeps,
