@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define SSM_ABI_VERSION 8
+#define SSM_ABI_VERSION 9
 
 /* error codes */
 #define SSM_OK 0
@@ -102,8 +102,10 @@ int ssm_abi_version(void);
 /* Thread-local text of the last error on this thread ("" if none). */
 const char* ssm_last_error(void);
 
-/* Bytes of the forward checkpoint buffer `ckpt` (states entering each block of
- * the scan's time axis), needed by ssm_bwd.  Returns 0 for an invalid desc. */
+/* Bytes of the forward residual buffer `ckpt`, needed by ssm_bwd: the states
+ * entering each block of the scan's time axis and, with SSM_GATE, y before the
+ * gate (B*L*D elements of the I/O type), from which ssm_bwd forms dz.  Opaque
+ * to callers.  Returns 0 for an invalid desc. */
 size_t ssm_ckpt_bytes(const ssm_desc_t* desc);
 
 /* Bytes of scratch `workspace` that ssm_fwd needs (per-segment carries of a

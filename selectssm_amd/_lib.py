@@ -32,7 +32,7 @@ SSM_ACT_NONE = 0
 SSM_ACT_SILU = 1
 SSM_ACT_RELU = 2
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 STATIC_SCRATCH_BYTES = 64 << 20  # SSM_STATIC_SCRATCH_BYTES: ssm_bwd_static's workspace
 

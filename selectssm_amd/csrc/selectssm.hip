@@ -145,6 +145,7 @@ struct FwdArgs {
   const T* z;
   T* y;
   float* ckpt;
+  T* ypre;       // gated residual: y before the gate, (B,L,D) in the output map (or null)
   float* agg_H;  // [B][nseg][N][D]: state at the end of each segment from a zero start
   float* agg_P;  // [B][nseg][N][D]: product of the segment's decays a_t
   int L, D, N, nblk;
@@ -159,8 +160,8 @@ struct FwdArgs {
 // the two calls of a launch (a select of the structs' addresses would copy
 // both to scratch memory; per-field selects of uniform values stay in SGPRs).
 #define SSM_FWD_FIELDS(X)                                                                                     \
-  X(u) X(delta) X(A) X(Bc) X(Cc) X(Dskip) X(z) X(y) X(ckpt) X(agg_H) X(agg_P) X(L) X(D) X(N) X(nblk) X(ldy) \
-  X(ldz) X(ldbc) X(seg_len) X(nseg) X(dstride) X(flags)
+  X(u) X(delta) X(A) X(Bc) X(Cc) X(Dskip) X(z) X(y) X(ckpt) X(ypre) X(agg_H) X(agg_P) X(L) X(D) X(N) X(nblk)  \
+  X(ldy) X(ldz) X(ldbc) X(seg_len) X(nseg) X(dstride) X(flags)
 template <typename T>
 __device__ __forceinline__ FwdArgs<T> pick_args(const FwdArgs<T>& a0, const FwdArgs<T>& a1, bool second) {
   FwdArgs<T> r;
@@ -380,6 +381,10 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
   // the reverse map at L-1-(t0+i) + (3 - yoff): a uniform row plus this offset
   const uint32_t yo = (uint32_t)(((rev ? 3 - yoff : yoff) * ldy + q) * sizeof(T));
   const uint32_t yrowb = (uint32_t)(ldy * sizeof(T));
+  // the gated residual, y before the gate: dense (B,L,D) rows in the output map
+  T* __restrict__ yp_b = EPI && p.ypre != nullptr ? p.ypre + (int64_t)b * L * D : nullptr;
+  const buf_t ryp = make_buf(yp_b != nullptr ? yp_b : y_b);
+  const uint32_t ypo = (uint32_t)(((rev ? 3 - yoff : yoff) * D + q) * sizeof(T));
   uint32_t cko[SPL];  // checkpoint offsets of this lane's states within a block
 #pragma unroll
   for (int j = 0; j < SPL; ++j) cko[j] = (uint32_t)(((SPL * g + j) * D + d) * sizeof(float));
@@ -398,9 +403,10 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
     // without per-lane predicates; tiles of a launch without checkpoints
     // (inference) skip their stores
     const bool full = full_cb && N == NS && t0 + kTT <= L;
-    auto tile = [&](auto full_tag, auto ck_tag) {
+    auto tile = [&](auto full_tag, auto ck_tag, auto yp_tag) {
       constexpr bool kFull = decltype(full_tag)::value;
       constexpr bool kCkpt = decltype(ck_tag)::value;
+      constexpr bool kYp = EPI && decltype(yp_tag)::value;  // store the gated residual
       // operands of steps i .. i + PF + 1 in a ring of PF + 2 register sets;
       // (u, delta) of two steps are read by one LDS instruction
       static_assert(PF % 2 == 0, "operands are prefetched in step pairs");
@@ -431,6 +437,8 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
       // running row offsets of the y and checkpoint stores (scalars)
       uint32_t yro = (uint32_t)(rev ? L - 4 - t0 : t0) * yrowb;
       const uint32_t ystep = rev ? 0u - 4u * yrowb : 4u * yrowb;
+      uint32_t ypro = (uint32_t)(rev ? L - 4 - t0 : t0) * rowb;
+      const uint32_t ypstep = rev ? 0u - 4u * rowb : 4u * rowb;
       uint32_t cro = (uint32_t)(t0 / kCK) * ckrowb;
 #pragma unroll
       for (int i = 0; i < kTT; ++i) {
@@ -486,6 +494,14 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
           const int ti = i - 3 + yoff;
           const int t = t0 + ti;
           yv = fmaf(uo, Dq, yv);
+          if constexpr (kYp) {
+            if constexpr (kFull) {
+              bst<T>(ryp, ypo, ypro, yv);
+              ypro += ypstep;
+            } else if (valid && t < L) {
+              bst<T>(ryp, (uint32_t)(rev ? L - 1 - t : t) * rowb + (uint32_t)(q * sizeof(T)), 0, yv);
+            }
+          }
           if constexpr (EPI) yv *= zo;
           if constexpr (kFull) {
             // row t0+i-3 (or L-1-(t0+i) >= 0 with the reverse map) plus the lane's yo
@@ -497,10 +513,18 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
         }
       }
     };
-    if (ck_b != nullptr) {
-      if (full) tile(std::true_type{}, std::true_type{}); else tile(std::false_type{}, std::true_type{});
+    constexpr std::true_type yes{};
+    constexpr std::false_type no{};
+    if (ck_b == nullptr) {
+      if (full) tile(yes, no, no); else tile(no, no, no);
+    } else if constexpr (EPI) {
+      if (yp_b != nullptr) {
+        if (full) tile(yes, yes, yes); else tile(no, yes, yes);
+      } else {
+        if (full) tile(yes, yes, no); else tile(no, yes, no);
+      }
     } else {
-      if (full) tile(std::true_type{}, std::false_type{}); else tile(std::false_type{}, std::false_type{});
+      if (full) tile(yes, yes, no); else tile(no, yes, no);
     }
     if (more) commit(buf ^ 1, t0 + kTT);
     __syncthreads();
@@ -686,6 +710,7 @@ struct BwdArgs {
   const float* Dskip;
   const T* z;
   const float* ckpt;
+  const T* ypre;  // gated residual: y before the gate, written by the forward (or null)
   const T* dy;
   T* du;
   T* ddelta;
@@ -706,9 +731,9 @@ struct BwdArgs {
 };
 
 #define SSM_BWD_FIELDS(X)                                                                                     \
-  X(u) X(delta) X(A) X(Bc) X(Cc) X(Dskip) X(z) X(ckpt) X(dy) X(du) X(ddelta) X(dz) X(ws_dB) X(ws_dC) X(ws_dA) \
-  X(ws_dD) X(ws_ddt) X(agg_G) X(agg_P) X(Bt) X(L) X(D) X(N) X(nblk) X(ncb) X(ldy) X(ldz) X(ldbc) X(seg_len)   \
-  X(nseg) X(dstride) X(flags)
+  X(u) X(delta) X(A) X(Bc) X(Cc) X(Dskip) X(z) X(ckpt) X(ypre) X(dy) X(du) X(ddelta) X(dz) X(ws_dB) X(ws_dC)  \
+  X(ws_dA) X(ws_dD) X(ws_ddt) X(agg_G) X(agg_P) X(Bt) X(L) X(D) X(N) X(nblk) X(ncb) X(ldy) X(ldz) X(ldbc)     \
+  X(seg_len) X(nseg) X(dstride) X(flags)
 template <typename T>
 __device__ __forceinline__ BwdArgs<T> pick_args(const BwdArgs<T>& a0, const BwdArgs<T>& a1, bool second) {
   BwdArgs<T> r;
@@ -779,12 +804,10 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
   // skip source map: its gradient reads the gated dy there, which is the lane's
   // own staged dy when S is the identity and another element otherwise
   const bool stage_dyo = EPI && skip && (srev || scomp);
-  const bool stage_eu = gate && skip && (srev || scomp);  // the skip's u inside y_pre for dz
   const bool mrev = rev != srev, mcomp = comp != scomp;   // O(S(t,d)) relative to (t,d)
   const bool dsp = p.flags & SSM_DELTA_SOFTPLUS;
   const int q = comp ? D - 1 - dc : dc;
   const float Dd = (skip && valid) ? p.Dskip[dc] : 0.0f;  // u[t,d] carries D[d] (selectssm.py:238)
-  const float Dq = (skip && valid) ? p.Dskip[scomp ? D - 1 - dc : dc] : 0.0f;  // the skip inside y_pre
   const int scol = tid & (kBlkCh - 1);
   const int srow0 = wave;  // = tid / kBlkCh: the staged rows of a wave are uniform
   const int sd = cb * kBlkCh + scol;
@@ -803,8 +826,6 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
   const float dmask = (is_du && lead) ? 1.0f : 0.0f;    // one lane per (step, channel) adds to dD
   // du / ddelta of step t0 + i + (1 - (orow & 1)) go to row t0 + i plus this offset
   const uint32_t oo = (uint32_t)((1 - (orow & 1)) * D + d);  // elements
-  // dz of step t0 + i - 3 + yrow_step(orow): row t0 + i - 3 (or L-1-(t0+i)) plus this offset
-  const uint32_t dzo = (uint32_t)(((rev ? 3 - yrow_step(orow) : yrow_step(orow)) * D + q) * sizeof(T));
 
   float Av[SPL], A2[SPL], gc[SPL], dAacc[SPL], dAmid[SPL];
 #pragma unroll
@@ -847,17 +868,15 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
   constexpr int kSB = (SPL == 4 && EPI) ? 1 : 2;
   int sb = 0;
   // the next block's staging commit runs between the block's two sweeps,
-  // except in the builds whose registers it would push into spills (the
-  // accumulating gated one and the gated N > 16 ones), where it follows them
-  constexpr bool kMidCommit = !ACC && !(SPL == 4 && EPI);
+  // except in the gated N > 16 builds (registers already spilled, one LDS set
+  // of channel sums), where it follows them
+  constexpr bool kMidCommit = !(SPL == 4 && EPI);
   // with two sets and the commit between the sweeps, a block's dB / dC totals
   // are added in the next block, after its commit, instead of right after the
   // block-end barrier, where every wave waited on the same LDS reads at once
   constexpr bool kLateTotals = kSB == 2 && kMidCommit;
   __shared__ float s_dB[kSB][kBwdWaves][kCK][NS], s_dC[kSB][kBwdWaves][kCK][NS];
-  __shared__ float s_go[EB][ER][kBlkCh], s_gz[EB][ER][kBlkCh];  // gate: raw dy and z at the output position
-  __shared__ float s_eu[EB][ER][kBlkCh], s_dyo[EB][ER][kBlkCh];
-  __shared__ float s_dza[EB][ER][kBlkCh];  // SSM_ACCUMULATE: dz before this call, at the output position
+  __shared__ float s_dyo[EB][ER][kBlkCh];  // skip map: the gated dy at O(S(t,d))
   __shared__ float s_ddt[kSB][kBwdWaves][kCK];  // broadcast delta: per-wave channel sums of ddelta
 
   const int dtD = p.dstride ? D : 1;
@@ -873,10 +892,11 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
   const float* __restrict__ ck_b = p.ckpt + (int64_t)b * p.nblk * N * D;
   T* __restrict__ out_b = (is_du ? p.du : p.ddelta) + (int64_t)b * L * D;  // ddelta only when (B,L,D)
   T* __restrict__ dz_b = EPI ? p.dz + (int64_t)b * L * D : nullptr;
+  const T* __restrict__ yp_b = EPI && p.ypre != nullptr ? p.ypre + (int64_t)b * L * D : nullptr;  // gated residual
 
   // fetch() only issues loads; commit() (between the block's sweeps, or after
   // them, kMidCommit) masks, applies softplus and the gate and writes LDS
-  stg<T> r_u[RPT], r_dt[RPT], r_dy[RPT], r_gz[RPT], r_eu[RPT], r_dyo[RPT], r_zo[RPT], r_dza[RPT];
+  stg<T> r_u[RPT], r_dt[RPT], r_dy[RPT], r_gz[RPT], r_yp[RPT], r_dyo[RPT], r_zo[RPT], r_dza[RPT];
   stg<T> r_B[BCE], r_C[BCE];
   float r_h[SPL];
   float h_next[SPL];  // checkpoint of the block staged by the last commit
@@ -885,7 +905,7 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
   const uint32_t so_q = (uint32_t)(sq * sizeof(T));
   const uint32_t so_dt = (uint32_t)(scol_dt * sizeof(T));
   const buf_t ru = make_buf(u_b), rdt = make_buf(dt_b), rdy = make_buf(dy_b), rB = make_buf(B_b), rC = make_buf(C_b);
-  const buf_t rck = make_buf(ck_b), rdz = make_buf(EPI ? dz_b : p.du);
+  const buf_t rck = make_buf(ck_b);
   const uint32_t rowb = (uint32_t)(D * sizeof(T));      // bytes per (B,L,D) row
   const uint32_t dyrowb = (uint32_t)(ldy * sizeof(T));  // bytes per dy row
   const uint32_t ckrowb = (uint32_t)(N * D * sizeof(float));
@@ -912,16 +932,17 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
         r_C[k] = bldr<T>(rC, o, 0);
       }
     }
-    if (gate || stage_eu || stage_dyo) {
+    if (gate || stage_dyo) {
 #pragma unroll
       for (int k = 0; k < RPT; ++k) {
         const int tc = min(t0 + srow0 + k * RSTEP, L - 1);
         const int pr = rev ? L - 1 - tc : tc;     // output row
-        const int prs = srev ? L - 1 - tc : tc;   // skip-source row
         const int prm = mrev ? L - 1 - tc : tc;   // row of O(S(.))
-        if (gate) r_gz[k] = ld32r(z_b, (uint32_t)(pr * ldz + sq));
+        if (gate) {
+          r_gz[k] = ld32r(z_b, (uint32_t)(pr * ldz + sq));
+          r_yp[k] = ld32r(yp_b, (uint32_t)(pr * D + sq));
+        }
         if (acc_dz) r_dza[k] = ld32r(dz_b, (uint32_t)(pr * D + sq));
-        if (stage_eu) r_eu[k] = ld32r(u_b, (uint32_t)(prs * D + sqs));
         if (stage_dyo) {
           r_dyo[k] = ld32r(dy_b, (uint32_t)(prm * ldy + sqm));
           if (gate) r_zo[k] = ld32r(z_b, (uint32_t)(prm * ldz + sqm));
@@ -943,10 +964,19 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
       float dyg = go;
       if (gate) {
         const float gz = in ? val(r_gz[k]) : 0.0f;
-        s_go[buf][i][scol] = go;
-        s_gz[buf][i][scol] = gz;
-        if (acc_dz) s_dza[buf][i][scol] = in ? val(r_dza[k]) : 0.0f;
-        dyg = go * gz * sigmoid(gz);
+        const float sgz = sigmoid(gz);
+        dyg = go * gz * sgz;
+        // dz = dy y_pre silu'(z), elementwise: y_pre is the forward's gated
+        // residual, at the output position of scan step t0 + i like dy and z
+        if (in) {
+          const int pr = rev ? L - 1 - (t0 + i) : t0 + i;
+          float dzv = go * val(r_yp[k]) * sgz * (1.0f + gz * (1.0f - sgz));
+          if (acc_dz) {
+            pin(dzv);  // rounded on its own, as a separate dz would be (no fused multiply-add)
+            dzv = val(r_dza[k]) + dzv;
+          }
+          st32(dz_b, (uint32_t)(pr * D + sq), dzv);
+        }
       }
       s_x[buf][i][scol] = in ? make_float4(val(r_u[k]), dtv, dyg, sg) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
@@ -960,7 +990,6 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
     for (int k = 0; k < RPT; ++k) {
       const int i = srow0 + k * RSTEP;
       const bool in = svalid && t0 + i < L;
-      if (stage_eu) s_eu[buf][i][scol] = in ? val(r_eu[k]) : 0.0f;
       if (stage_dyo) {
         float v = in ? val(r_dyo[k]) : 0.0f;
         if (gate) {
@@ -1028,14 +1057,13 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
 #pragma unroll
     for (int j = 0; j < SPL; ++j) dAblk[j] = 0.0f;
     float dDblk = 0.0f;
-    // the gate and the skip / softplus terms are compile-time properties of
-    // each instance of the sweeps (branches in the unrolled step loop would
-    // split it into many small scheduling regions)
-    auto sweeps = [&](auto full_tag, auto gate_tag, auto sd_tag) {
+    // the skip / softplus terms are a compile-time property of each instance
+    // of the sweeps (branches in the unrolled step loop would split it into
+    // many small scheduling regions); the gate is no longer in the sweeps: dz
+    // is formed elementwise in the staging, from the forward's residual
+    auto sweeps = [&](auto full_tag, auto sd_tag) {
       constexpr bool kFull = decltype(full_tag)::value;
-      constexpr bool kGate = EPI && decltype(gate_tag)::value;
       constexpr bool kSD = decltype(sd_tag)::value;  // skip || dsp
-      constexpr bool kAccDz = ACC && kGate;
       float a_s[kCK][SPL], hp_s[kCK][SPL];
       // (u, delta, dy) and B of the block kept in registers from the
       // recompute for the adjoint where they fit (2 states per lane): the
@@ -1060,25 +1088,13 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
           lds_vec<2 * SPL>(&s_bc[buf][i][g][sig][0], bc[i % R]);
         }
       };
-      // forward recompute of the block: a_t, h_{t-1}; dC_t = sum_d dy_t h_t;
-      // with the gate, y_t for dz
+      // forward recompute of the block: a_t, h_{t-1}; dC_t = sum_d dy_t h_t
 #pragma unroll
       for (int i = 0; i < PF; ++i) pre(i, std::false_type{});
-      float yp[4];
       float vCp[SPL], vBp[SPL];  // (SSM_BWD_PIPE) the previous step's products
-      // gate: operands of the current 4-step group at this lane's output
-      // step, read at the group's first step
-      float ge_u = 0.0f, ge_z = 0.0f, ge_o = 0.0f, ge_a = 0.0f;
 #pragma unroll
       for (int i = 0; i < kCK; ++i) {
         if (i + PF < kCK) pre(i + PF, std::false_type{});
-        if (kGate && (i & 3) == 0) {
-          const int ti = i + yrow_step(orow);
-          if (skip) ge_u = stage_eu ? s_eu[buf][ti][cw] : s_x[buf][ti][cw].x;
-          ge_z = s_gz[buf][ti][cw];
-          ge_o = s_go[buf][ti][cw];
-          if constexpr (kAccDz) ge_a = s_dza[buf][ti][cw];
-        }
         __builtin_amdgcn_sched_barrier(0);
         const float uu = xr[i % R].x, dd = xr[i % R].y, dyv = xr[i % R].z;
         if constexpr (kKeepX) x_s[i] = make_float3(uu, dd, dyv);
@@ -1103,32 +1119,6 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
           if (i == kCK - 1) s_dC[sb][wave][i][SPL * g + sig] = chan_reduce8<SPL>(vCp);
         } else {
           s_dC[sb][wave][i][SPL * g + sig] = chan_reduce8<SPL>(vC);
-        }
-        if constexpr (kGate) {
-          float ys = bc[i % R][SPL] * h[0];
-#pragma unroll
-          for (int j = 1; j < SPL; ++j) ys = fmaf(bc[i % R][SPL + j], h[j], ys);
-          yp[i & 3] = ys;
-          if ((i & 3) == 3) {
-            float yv = rows_transpose_sum4(yp[0], yp[1], yp[2], yp[3]);
-            yv += dpp_mov<kDppRor8>(yv);
-            const int ti = i - 3 + yrow_step(orow);
-            const int t = t0 + ti;
-            if (skip) yv = fmaf(ge_u, Dq, yv);
-            const float zz = ge_z;
-            const float sg = sigmoid(zz);
-            float dzv = ge_o * yv * sg * (1.0f + zz * (1.0f - sg));
-            if constexpr (kAccDz) {
-              pin(dzv);  // rounded on its own, as a separate dz would be (no fused multiply-add)
-              dzv = ge_a + dzv;
-            }
-            // both halves of the row hold the value; both store it
-            if constexpr (kFull) {
-              bst<T>(rdz, dzo, (uint32_t)(rev ? L - 1 - t0 - i : t0 + i - 3) * rowb, dzv);
-            } else if (valid && t < L) {
-              bst<T>(rdz, (uint32_t)(rev ? L - 1 - t : t) * rowb + (uint32_t)(q * sizeof(T)), 0, dzv);
-            }
-          }
         }
       }
       // The next block's operands go to LDS here, between the sweeps (that
@@ -1219,17 +1209,10 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
         }
       }
     };
-    auto run_sweeps = [&](auto gate_tag, auto sd_tag) {
-      if (full) sweeps(std::true_type{}, gate_tag, sd_tag); else sweeps(std::false_type{}, gate_tag, sd_tag);
+    auto run_sweeps = [&](auto sd_tag) {
+      if (full) sweeps(std::true_type{}, sd_tag); else sweeps(std::false_type{}, sd_tag);
     };
-    auto run_sd = [&](auto gate_tag) {
-      if (skip || dsp) run_sweeps(gate_tag, std::true_type{}); else run_sweeps(gate_tag, std::false_type{});
-    };
-    if constexpr (EPI) {
-      if (gate) run_sd(std::true_type{}); else run_sd(std::false_type{});
-    } else {
-      run_sd(std::false_type{});
-    }
+    if (skip || dsp) run_sweeps(std::true_type{}); else run_sweeps(std::false_type{});
 #pragma unroll
     for (int j = 0; j < SPL; ++j) dAmid[j] += dAblk[j];
     dDmid += dDblk;
@@ -1640,6 +1623,13 @@ bool dispatch_spl(int spl, bool epi, F&& f) {
 }
 
 size_t ckpt_floats(const Shape& s) { return (size_t)s.B * s.nblk * s.N * s.D; }
+// The forward's residuals are its checkpoints, then (with SSM_GATE) y before
+// the gate: (B,L,D) of the I/O type in the output map, from which the backward
+// forms dz elementwise instead of recomputing y = C h
+size_t ypre_bytes(const ssm_desc_t* desc, const Shape& s) {
+  if (!(desc->flags & SSM_GATE)) return 0;
+  return (size_t)s.B * s.L * s.D * (desc->dtype == SSM_F32 ? sizeof(float) : sizeof(uint16_t));
+}
 
 // Per-segment aggregates of a time-split scan: [B][nseg][N][D] states (or
 // adjoint carries) then [B][nseg][N][D] decay products.  None for one segment.
@@ -1678,6 +1668,7 @@ FwdArgs<T> fwd_args(const ssm_desc_t* desc, const Shape& s, const void* u, const
   a.z = static_cast<const T*>(z);
   a.y = static_cast<T*>(y);
   a.ckpt = ckpt;
+  a.ypre = ckpt != nullptr && (desc->flags & SSM_GATE) ? reinterpret_cast<T*>(ckpt + ckpt_floats(s)) : nullptr;
   a.agg_H = static_cast<float*>(workspace);
   a.agg_P = a.agg_H + (s.nseg > 1 ? (size_t)s.B * s.nseg * s.N * s.D : 0);
   a.L = s.L;
@@ -1764,6 +1755,7 @@ BwdArgs<T> bwd_args(const ssm_desc_t* desc, const Shape& s, const void* u, const
   a.Dskip = Dskip;
   a.z = static_cast<const T*>(z);
   a.ckpt = ckpt;
+  a.ypre = (desc->flags & SSM_GATE) ? reinterpret_cast<const T*>(ckpt + ckpt_floats(s)) : nullptr;
   a.dy = static_cast<const T*>(dy);
   a.du = static_cast<T*>(du);
   a.ddelta = static_cast<T*>(ddelta);
@@ -1935,7 +1927,7 @@ size_t ssm_ckpt_bytes(const ssm_desc_t* desc) {
   g_last_error.clear();
   Shape s;
   if (validate(desc, &s)) return 0;
-  return ckpt_floats(s) * sizeof(float);
+  return ckpt_floats(s) * sizeof(float) + ypre_bytes(desc, s);
 }
 
 size_t ssm_fwd_workspace_bytes(const ssm_desc_t* desc) {

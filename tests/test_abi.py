@@ -47,6 +47,12 @@ def test_size_queries():
     d = L.make_desc(8, 8192, 2048, 16)
     # checkpoints: one f32 state per (b, block of 16 steps, n, d)
     assert lib.ssm_ckpt_bytes(ctypes.byref(d)) == 8 * (8192 // 16) * 16 * 2048 * 4
+    # with the gate, y before the gate follows: B*L*D elements of the I/O type
+    for dt, w in ((L.SSM_F32, 4), (L.SSM_BF16, 2)):
+        g = L.make_desc(8, 8192, 2048, 16, dtype=dt, flags=L.SSM_GATE)
+        assert lib.ssm_ckpt_bytes(ctypes.byref(g)) == 8 * (8192 // 16) * 16 * 2048 * 4 + 8 * 8192 * 2048 * w
+        s = L.make_desc(8, 8192, 2048, 16, dtype=dt, flags=L.SSM_SKIP)
+        assert lib.ssm_ckpt_bytes(ctypes.byref(s)) == 8 * (8192 // 16) * 16 * 2048 * 4
     assert lib.ssm_bwd_workspace_bytes(ctypes.byref(d)) > 0
     bad = L.make_desc(8, 8192, 2048, 33)
     assert lib.ssm_ckpt_bytes(ctypes.byref(bad)) == 0
