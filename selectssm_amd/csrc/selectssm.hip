@@ -1628,7 +1628,8 @@ size_t ckpt_floats(const Shape& s) { return (size_t)s.B * s.nblk * s.N * s.D; }
 // forms dz elementwise instead of recomputing y = C h
 size_t ypre_bytes(const ssm_desc_t* desc, const Shape& s) {
   if (!(desc->flags & SSM_GATE)) return 0;
-  return (size_t)s.B * s.L * s.D * (desc->dtype == SSM_F32 ? sizeof(float) : sizeof(uint16_t));
+  const size_t n = (size_t)s.B * s.L * s.D * (desc->dtype == SSM_F32 ? sizeof(float) : sizeof(uint16_t));
+  return (n + 15) / 16 * 16;  // the buffer stays a whole number of floats (and 16-byte granules)
 }
 
 // Per-segment aggregates of a time-split scan: [B][nseg][N][D] states (or

@@ -53,6 +53,9 @@ def test_size_queries():
         assert lib.ssm_ckpt_bytes(ctypes.byref(g)) == 8 * (8192 // 16) * 16 * 2048 * 4 + 8 * 8192 * 2048 * w
         s = L.make_desc(8, 8192, 2048, 16, dtype=dt, flags=L.SSM_SKIP)
         assert lib.ssm_ckpt_bytes(ctypes.byref(s)) == 8 * (8192 // 16) * 16 * 2048 * 4
+    # an odd bf16 residual is rounded up to whole 16-byte granules
+    odd = L.make_desc(1, 3, 5, 4, dtype=L.SSM_BF16, flags=L.SSM_GATE)
+    assert lib.ssm_ckpt_bytes(ctypes.byref(odd)) == 1 * 1 * 4 * 5 * 4 + 32
     assert lib.ssm_bwd_workspace_bytes(ctypes.byref(d)) > 0
     bad = L.make_desc(8, 8192, 2048, 33)
     assert lib.ssm_ckpt_bytes(ctypes.byref(bad)) == 0
