@@ -806,7 +806,6 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
   const bool stage_dyo = EPI && skip && (srev || scomp);
   const bool mrev = rev != srev, mcomp = comp != scomp;   // O(S(t,d)) relative to (t,d)
   const bool dsp = p.flags & SSM_DELTA_SOFTPLUS;
-  const int q = comp ? D - 1 - dc : dc;
   const float Dd = (skip && valid) ? p.Dskip[dc] : 0.0f;  // u[t,d] carries D[d] (selectssm.py:238)
   const int scol = tid & (kBlkCh - 1);
   const int srow0 = wave;  // = tid / kBlkCh: the staged rows of a wave are uniform
@@ -814,7 +813,6 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
   const bool svalid = sd < D;
   const int sdc = svalid ? sd : 0;
   const int sq = comp ? D - 1 - sdc : sdc;     // output channel of the staged column
-  const int sqs = scomp ? D - 1 - sdc : sdc;   // skip-source channel
   const int sqm = mcomp ? D - 1 - sdc : sdc;   // channel of O(S(.)) for the skip's gradient
   const bool full_cb = (cb + 1) * kBlkCh <= D;
   // after the exchange over state groups, row g >> 1 of the wave holds
