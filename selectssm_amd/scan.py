@@ -214,7 +214,9 @@ def scan_fwd(u, delta, A, B, C, Dskip=None, z=None, reverse=False, complement=Fa
     may be column slices of one array (:func:`bc_stride`).  ``reverse`` /
     ``complement`` map the output (independently) and ``skip_map`` the skip's
     source (:func:`_flags`).
-    Returns ``(y, ckpt)``; ``ckpt`` is None when ``want_ckpt`` is False.
+    Returns ``(y, ckpt)``: ``ckpt`` is the residual buffer :func:`scan_bwd` needs
+    (the states entering each 16-step block and, with the gate, y before the
+    gate), or None when ``want_ckpt`` is False.
     """
     flags = _flags(Dskip is not None, z is not None, reverse, complement, delta_softplus, skip_map)
     y = torch.empty_like(u) if y_out is None else y_out
