@@ -40,9 +40,9 @@
 // i + PF are read while step i computes (sched_barrier keeps the reads where
 // they are written).  Staged bf16 values stay raw 16-bit registers until they
 // are written to LDS (a widening next to the load would wait for it there).
-// With 2 states per lane
-// the backward keeps the block's (u, delta, dy) and B in registers from its
-// recompute sweep, so the adjoint sweep reads only C from LDS.  Sums
+// With 2 states per lane the backward keeps the block's (u, delta, dy) and
+// (without the gate) B in registers from its recompute sweep, so the adjoint
+// sweep reads only C from LDS.  Sums
 // over channel blocks (dB, dC, broadcast ddelta) and over rows / segments
 // (dA, dD) go through partial buffers reduced in a fixed order, so every
 // gradient is deterministic.
@@ -754,10 +754,10 @@ struct BwdStage {
 // channels in reverse, starting from the adjoint carry the later segments
 // hand over (ssm_bwd_agg_kernel), and writes du, ddelta, dz and the partial
 // sums of dB, dC, dA, dD (and of a broadcast ddelta).
-// SPL: states per lane (N <= 8 * SPL).  EPI: the gate and the reverse skip.
-// BC: delta is (B,L,1), shared by the channels.  ACC (with EPI): dz += the
-// gate's gradient (SSM_ACCUMULATE), a build of its own so that the plain
-// gated backward keeps its registers.
+// SPL: states per lane (N <= 8 * SPL).  EPI: the gate (dz formed in the
+// staging pass from the forward's residual y before the gate) and skip source
+// maps.  BC: delta is (B,L,1), shared by the channels.  ACC (with EPI): dz +=
+// the gate's gradient (SSM_ACCUMULATE), a build of its own.
 // Rows of p0 below rows0, rows of p1 above, as ssm_fwd_kernel.
 template <int SPL, bool EPI, bool BC, bool ACC, typename T>
 __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T> p0, BwdArgs<T> p1, int rows0) {
