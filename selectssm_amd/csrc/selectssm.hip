@@ -198,8 +198,6 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
   constexpr int NT = FwdStage::NT, RPT = FwdStage::RPT, RSTEP = FwdStage::RSTEP;
   constexpr int BCN = kTT * NS;                 // staged B (or C) elements per tile
   constexpr int BCE = (BCN + NT - 1) / NT;      // per thread
-  constexpr int EB = EPI ? 2 : 1;
-  constexpr int ER = EPI ? kTT : 1;
   constexpr int PF = SSM_FWD_PF;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -225,7 +223,7 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
   const bool srev = smap ? (p.flags & SSM_SKIP_REVERSE) != 0 : rev;
   const bool scomp = smap ? (p.flags & SSM_SKIP_COMPLEMENT) != 0 : comp;
   // the skip from the scan position uses the staged u itself; any other skip
-  // source and the gate need the extra staging of EPI builds
+  // source and the gate need the extra per-lane loads of EPI builds
   const bool skip = (p.flags & SSM_SKIP) != 0;
   const bool gate = EPI && (p.flags & SSM_GATE);
   const bool stage_eu = EPI && skip && (srev || scomp);  // the skip's u is another element
@@ -236,8 +234,6 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
   const int sd = cb * kBlkCh + scol;
   const bool svalid = sd < D;
   const int sdc = svalid ? sd : 0;
-  const int sq = comp ? D - 1 - sdc : sdc;     // output channel of the staged column (z)
-  const int sqs = scomp ? D - 1 - sdc : sdc;   // skip-source channel of the staged column (u)
   const bool full_cb = (cb + 1) * kBlkCh <= D;
 
   float A2[SPL], h[SPL];
@@ -265,7 +261,6 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
   }
 
   __shared__ float2 s_ud[2][kTT][kBlkCh];  // (u, delta)
-  __shared__ float s_eu[EB][ER][kBlkCh], s_ez[EB][ER][kBlkCh];
   __shared__ __attribute__((aligned(16))) float s_B[2][kTT][NS];
   __shared__ __attribute__((aligned(16))) float s_C[2][kTT][NS];
 
@@ -283,8 +278,7 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
   const int ND = N * D;
   const buf_t ru = make_buf(u_b), rdt = make_buf(dt_b), rB = make_buf(B_b), rC = make_buf(C_b);
   const buf_t rz = make_buf(EPI ? z_b : u_b), ry = make_buf(y_b), rck = make_buf(ck_b != nullptr ? ck_b : p.A);
-  const uint32_t cb_c = (uint32_t)(sdc * sizeof(T)), cb_q = (uint32_t)(sq * sizeof(T));
-  const uint32_t cb_qs = (uint32_t)(sqs * sizeof(T));
+  const uint32_t cb_c = (uint32_t)(sdc * sizeof(T));
   const uint32_t cb_dt = (uint32_t)(scol_dt * sizeof(T));
 
   // fetch() only issues loads (clamped addresses, raw values); commit(), run
@@ -292,7 +286,17 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
   // LDS, so the loads' latency is covered by a whole tile.  VEC launches read
   // u and delta as 4-element vectors: thread -> rows vr, vr + 16, channels
   // vc .. vc + 3 (D % 4 == 0, so a vector is wholly inside or outside D).
-  stg<T> r_u[RPT], r_dt[RPT], r_eu[RPT], r_ez[RPT], r_B[BCE], r_C[BCE];
+  stg<T> r_u[RPT], r_dt[RPT], r_B[BCE], r_C[BCE];
+  // EPI builds: z (gate) and the skip's u at another element (skip maps) at
+  // this lane's own output steps of the tile, one per 4-step group, loaded by
+  // the fetch straight into registers (no LDS staging: the gated forward keeps
+  // the plain forward's LDS size, and so its waves per SIMD) and converted by
+  // the commit
+  constexpr int KG = EPI ? kTT / 4 : 1;
+  const int yoff = yrow_step(g);  // step of each 4-step group this lane's row ends with
+  const uint32_t lq = (uint32_t)(q * sizeof(T)), lqs = (uint32_t)((scomp ? D - 1 - dc : dc) * sizeof(T));
+  stg<T> zn[KG], en[KG];
+  float zc[KG], ec[KG];
   constexpr int VK = kTT / 16;  // vector rows per thread
   stg4<T> v_u[VK], v_dt[VK];
   static_assert(NT == 256 && kTT % 16 == 0, "vector staging: 16 threads per row, 16 rows per pass");
@@ -326,14 +330,16 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
         r_C[k] = bldr<T>(rC, o, 0);
       }
     }
-    if (stage_eu || gate) {
+    if constexpr (EPI) {
+      if (stage_eu || gate) {
 #pragma unroll
-      for (int k = 0; k < RPT; ++k) {
-        const int tc = min(t0 + srow0 + k * RSTEP, L - 1);
-        const int pr = rev ? L - 1 - tc : tc;    // output row (z)
-        const int prs = srev ? L - 1 - tc : tc;  // skip-source row (u)
-        if (stage_eu) r_eu[k] = bldr<T>(ru, cb_qs, (uint32_t)prs * rowb);
-        if (gate) r_ez[k] = bldr<T>(rz, cb_q, (uint32_t)(pr * ldz * sizeof(T)));
+        for (int k = 0; k < KG; ++k) {
+          const int tc = min(t0 + 4 * k + yoff, L - 1);  // this lane's output step of group k
+          const int pr = rev ? L - 1 - tc : tc;    // output row (z)
+          const int prs = srev ? L - 1 - tc : tc;  // skip-source row (u)
+          if (stage_eu) en[k] = bldr<T>(ru, lqs, (uint32_t)prs * rowb);
+          if (gate) zn[k] = bldr<T>(rz, lq, (uint32_t)(pr * ldz * sizeof(T)));
+        }
       }
     }
   };
@@ -357,12 +363,12 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
         s_ud[buf][i][scol] = in ? make_float2(val(r_u[k]), dv) : make_float2(0.0f, 0.0f);
       }
     }
+    if constexpr (EPI) {
 #pragma unroll
-    for (int k = 0; k < RPT; ++k) {
-      const int i = srow0 + k * RSTEP;
-      const bool in = svalid && t0 + i < L;
-      if (stage_eu) s_eu[buf][i][scol] = in ? val(r_eu[k]) : 0.0f;
-      if (gate) s_ez[buf][i][scol] = in ? val(r_ez[k]) : 0.0f;
+      for (int k = 0; k < KG; ++k) {
+        zc[k] = gate ? val(zn[k]) : 0.0f;
+        ec[k] = stage_eu ? val(en[k]) : 0.0f;
+      }
     }
 #pragma unroll
     for (int k = 0; k < BCE; ++k) {
@@ -376,7 +382,6 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
     }
   };
 
-  const int yoff = yrow_step(g);  // step of each 4-step group this lane's row ends with
   // y of step t0 + i - 3 + yoff is stored at row t0 + i - 3 + yoff, or with
   // the reverse map at L-1-(t0+i) + (3 - yoff): a uniform row plus this offset
   const uint32_t yo = (uint32_t)(((rev ? 3 - yoff : yoff) * ldy + q) * sizeof(T));
@@ -448,10 +453,11 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
           // reverse map makes another element (staged in EPI builds)
           const int ti = i + yoff;
           if constexpr (EPI) {
-            // branch-free: one read from either array; z is read (and
-            // discarded below) without the gate as well
-            uo = *(stage_eu ? &s_eu[buf][ti][cw] : &s_ud[buf][ti][cw].x);
-            zo = s_ez[buf][ti][cw];
+            // z and the skip's u at another element come from registers; z is
+            // taken (and discarded below) without the gate as well
+            const float us = s_ud[buf][ti][cw].x;
+            uo = stage_eu ? ec[i >> 2] : us;
+            zo = zc[i >> 2];
           } else {
             uo = s_ud[buf][ti][cw].x;
           }
