@@ -160,6 +160,18 @@ __device__ __forceinline__ bool barrier_any(bool v, int* flags) {
   return any != 0;
 }
 
+// The bitwise OR over the NW waves of a workgroup of a wave-uniform int v,
+// barrier and slots as in barrier_any.
+template <int NW>
+__device__ __forceinline__ int barrier_or(int v, int* flags) {
+  if ((threadIdx.x & 63) == 0) flags[threadIdx.x >> 6] = v;
+  __syncthreads();
+  int any = 0;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) any |= flags[i];
+  return any;
+}
+
 // Keeps v computed at this point of the program: an empty asm statement that
 // reads and writes v in a VGPR and emits no instruction.  Arithmetic feeding
 // it cannot be moved past it, so a walk whose results are used only after a

@@ -152,6 +152,8 @@ struct FwdArgs {
   int ldy, ldz;       // row strides (elements) of y and z
   int ldbc;           // row stride (elements) of B and C
   int seg_len, nseg;  // time segments per row (seg_len a multiple of kTT)
+  int asub;           // aggregate walks per segment (agg_H / agg_P: [B][nseg * asub][N][D])
+  int* aflag;         // [B][nseg * asub][ncb] with asub > 1 (else null): 1 once a piece's products are all 0
   int dstride;        // 1, or 0 for a (B,L,1) delta
   uint32_t flags;
 };
@@ -161,7 +163,7 @@ struct FwdArgs {
 // both to scratch memory; per-field selects of uniform values stay in SGPRs).
 #define SSM_FWD_FIELDS(X)                                                                                     \
   X(u) X(delta) X(A) X(Bc) X(Cc) X(Dskip) X(z) X(y) X(ckpt) X(ypre) X(agg_H) X(agg_P) X(L) X(D) X(N) X(nblk)  \
-  X(ldy) X(ldz) X(ldbc) X(seg_len) X(nseg) X(dstride) X(flags)
+  X(ldy) X(ldz) X(ldbc) X(seg_len) X(nseg) X(asub) X(aflag) X(dstride) X(flags)
 template <typename T>
 __device__ __forceinline__ FwdArgs<T> pick_args(const FwdArgs<T>& a0, const FwdArgs<T>& a1, bool second) {
   FwdArgs<T> r;
@@ -244,11 +246,12 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
     h[j] = 0.0f;
   }
   if (seg > 0) {
-    // state entering this segment: h = P h + H over the earlier segments in
-    // order (the combine of selectssm.py:81-85 applied to whole segments)
-    const int64_t base = (int64_t)b * p.nseg * N * D + dc;
+    // state entering this segment: h = P h + H over the earlier segments'
+    // aggregate pieces in order (the combine of selectssm.py:81-85 applied to
+    // whole pieces)
+    const int64_t base = (int64_t)b * p.nseg * p.asub * N * D + dc;
 #pragma unroll 2
-    for (int s = 0; s < seg; ++s) {
+    for (int s = 0; s < seg * p.asub; ++s) {
 #pragma unroll
       for (int j = 0; j < SPL; ++j) {
         const int64_t o = base + ((int64_t)s * N + min(SPL * g + j, N - 1)) * D;
@@ -546,6 +549,15 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
 // P of the workgroup is 0 (flushed at tile ends, flush_tiny) all earlier
 // steps add exact zeros and the walk stops there: with decaying states only
 // the last few thousand steps of a long segment are read.
+//
+// With asub > 1 the segment is walked in asub pieces (workgroup z: piece
+// index), each into its own (H, P); the main pass folds them in order.  When
+// a piece's products all end at 0 it raises its flag, and the piece before
+// it in the segment, whose contributions reach the segment's end only through
+// those products (an exact 0 times a finite value), stops and writes H = P = 0:
+// the fold then gives the same floats.  The pieces at the segments' ends are
+// dispatched first, so with fast decays the earlier ones mostly stop after
+// one tile instead of each walking until its own products flush.
 template <int SPL, bool SP, typename T>
 __device__ __forceinline__ void fwd_agg_body(const FwdArgs<T>& p, const int b) {
   constexpr int NS = 4 * SPL;
@@ -560,10 +572,18 @@ __device__ __forceinline__ void fwd_agg_body(const FwdArgs<T>& p, const int b) {
   const int g = lane >> 4;
   // b: the batch row (blockIdx.y of a single launch)
   const int cb = blockIdx.x;
-  const int seg = blockIdx.z;
+  // blockIdx.z = (asub - 1 - part) * (nseg - 1) + segment, for segments
+  // 0 .. nseg - 2: every segment's last piece first
+  const int nsg = p.nseg - 1;
+  const int zq = blockIdx.z / nsg;
+  const int part = p.asub - 1 - zq;
+  const int seg = (blockIdx.z - zq * nsg) * p.asub + part;  // aggregate piece of the row
   const int L = p.L, D = p.D, N = p.N;
-  const int t_lo = seg * p.seg_len;
-  const int t_hi = min(L, t_lo + p.seg_len);
+  const int alen = p.seg_len / p.asub;
+  const int t_lo = seg * alen;
+  const int t_hi = min(L, t_lo + alen);
+  int* const fl = p.aflag ? p.aflag + ((int64_t)b * p.nseg * p.asub + seg) * gridDim.x + cb : nullptr;
+  const int* const fnext = fl && part < p.asub - 1 ? fl + gridDim.x : nullptr;  // the next piece's flag
   const int cw = wave * 16 + c;
   const int d = cb * kBlkCh + cw;
   const bool valid = d < D;
@@ -637,9 +657,11 @@ __device__ __forceinline__ void fwd_agg_body(const FwdArgs<T>& p, const int b) {
   fetch(t_last);
   commit(0, t_last);
   __syncthreads();
-  int buf = 0;
+  int buf = 0, vote = 0;
   for (int t0 = t_last;; t0 -= kTT, buf ^= 1) {
     const bool more = t0 > t_lo;
+    // read now, used at the tile's end: the load's latency hides behind the tile
+    const bool nflush = fnext && __hip_atomic_load(fnext, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
     if (more) fetch(t0 - kTT);
     constexpr int R = PF + 1;
     float2 ud[R];
@@ -681,16 +703,21 @@ __device__ __forceinline__ void fwd_agg_body(const FwdArgs<T>& p, const int b) {
     bool alive = false;
 #pragma unroll
     for (int j = 0; j < SPL; ++j) alive = alive || (live[j] && P[j] != 0.0f);
-    if (!barrier_any<kFwdWaves>(alive, s_alive[buf]) || !more) break;
+    // bit 0: a product of the workgroup is still live; bit 1: the next piece's are all 0
+    vote = barrier_or<kFwdWaves>((__ballot(alive) != 0 ? 1 : 0) | (nflush ? 2 : 0), s_alive[buf]);
+    if (vote != 1 || !more) break;
   }
-  const int64_t o = (int64_t)b * p.nseg + seg;
+  const bool stop = (vote & 2) != 0;
+  const int64_t o = (int64_t)b * p.nseg * p.asub + seg;
 #pragma unroll
   for (int j = 0; j < SPL; ++j) {
     if (live[j]) {
-      p.agg_H[(o * N + SPL * g + j) * D + d] = H[j];
-      p.agg_P[(o * N + SPL * g + j) * D + d] = P[j];
+      p.agg_H[(o * N + SPL * g + j) * D + d] = stop ? 0.0f : H[j];
+      p.agg_P[(o * N + SPL * g + j) * D + d] = stop ? 0.0f : P[j];
     }
   }
+  if (fl && (stop || (vote & 1) == 0) && tid == 0)
+    __hip_atomic_store(fl, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Workgroups with blockIdx.y < rows0 aggregate rows of p0, the others rows of
@@ -732,6 +759,8 @@ struct BwdArgs {
   int ldy, ldz;   // row strides (elements) of dy and of z
   int ldbc;       // row stride (elements) of B and C
   int seg_len, nseg;
+  int asub;    // aggregate walks per segment (agg_G / agg_P: [B][nseg * asub][N][D])
+  int* aflag;  // [B][nseg * asub][ncb] with asub > 1 (else null): 1 once a piece's products are all 0
   int dstride;
   uint32_t flags;
 };
@@ -739,7 +768,7 @@ struct BwdArgs {
 #define SSM_BWD_FIELDS(X)                                                                                     \
   X(u) X(delta) X(A) X(Bc) X(Cc) X(Dskip) X(z) X(ckpt) X(ypre) X(dy) X(du) X(ddelta) X(dz) X(ws_dB) X(ws_dC)  \
   X(ws_dA) X(ws_dD) X(ws_ddt) X(agg_G) X(agg_P) X(Bt) X(L) X(D) X(N) X(nblk) X(ncb) X(ldy) X(ldz) X(ldbc)     \
-  X(seg_len) X(nseg) X(dstride) X(flags)
+  X(seg_len) X(nseg) X(asub) X(aflag) X(dstride) X(flags)
 template <typename T>
 __device__ __forceinline__ BwdArgs<T> pick_args(const BwdArgs<T>& a0, const BwdArgs<T>& a1, bool second) {
   BwdArgs<T> r;
@@ -842,11 +871,11 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
   }
   if (seg < p.nseg - 1) {
     // adjoint carry entering this segment from the right: g = P g + G over the
-    // later segments, last segment first (g = a_t f_t at each segment's first
+    // later segments' aggregate pieces, last first (g = a_t f_t at each piece's first
     // step is linear in the carry it receives)
-    const int64_t base = (int64_t)b * p.nseg * N * D + dc;
+    const int64_t base = (int64_t)b * p.nseg * p.asub * N * D + dc;
 #pragma unroll 2
-    for (int s = p.nseg - 1; s > seg; --s) {
+    for (int s = p.nseg * p.asub - 1; s >= (seg + 1) * p.asub; --s) {
 #pragma unroll
       for (int j = 0; j < SPL; ++j) {
         const int64_t o = base + ((int64_t)s * N + min(nj[j], N - 1)) * D;
@@ -1278,7 +1307,9 @@ __global__ void __launch_bounds__(kWave* kBwdWaves, 1) ssm_bwd_kernel(BwdArgs<T>
 // product of the decays before the tile; G += P times the tile's own sum, then
 // P *= the tile's decay), so once every P of the workgroup is 0 (flushed at
 // tile ends, flush_tiny) all later steps add exact zeros and the walk stops
-// there.
+// there.  Pieces (asub > 1) as in the forward aggregate pass, mirrored: a
+// piece whose products all end at 0 lets the piece after it stop, and the
+// segments' first pieces are dispatched first.
 template <int SPL, bool EPI, typename T>
 __device__ __forceinline__ void bwd_agg_body(const BwdArgs<T>& p, const int b) {
   constexpr int NS = 8 * SPL;
@@ -1295,10 +1326,17 @@ __device__ __forceinline__ void bwd_agg_body(const BwdArgs<T>& p, const int b) {
   const int g = lane >> 3;
   // b: the batch row (blockIdx.y of a single launch)
   const int cb = blockIdx.x;
-  const int seg = blockIdx.z + 1;
+  // blockIdx.z = part * (nseg - 1) + segment - 1, for segments 1 .. nseg - 1:
+  // every segment's first piece first
+  const int nsg = p.nseg - 1;
+  const int part = blockIdx.z / nsg;
+  const int seg = (1 + blockIdx.z - part * nsg) * p.asub + part;  // aggregate piece of the row
   const int L = p.L, D = p.D, N = p.N;
-  const int t_lo = seg * p.seg_len;
-  const int t_hi = min(L, t_lo + p.seg_len);
+  const int alen = p.seg_len / p.asub;
+  const int t_lo = seg * alen;
+  const int t_hi = min(L, t_lo + alen);
+  int* const fl = p.aflag ? p.aflag + ((int64_t)b * p.nseg * p.asub + seg) * gridDim.x + cb : nullptr;
+  const int* const fprev = fl && part > 0 ? fl - gridDim.x : nullptr;  // the previous piece's flag
   const int cw = wave * 8 + c;
   const int d = cb * kBlkCh + cw;
   const bool valid = d < D;
@@ -1386,9 +1424,10 @@ __device__ __forceinline__ void bwd_agg_body(const BwdArgs<T>& p, const int b) {
   fetch(t_lo);
   commit(0, t_lo);
   __syncthreads();
-  int buf = 0;
+  int buf = 0, vote = 0;
   for (int t0 = t_lo;; t0 += kTT, buf ^= 1) {
     const bool more = t0 + kTT < t_hi;
+    const bool pflush = fprev && __hip_atomic_load(fprev, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
     if (more) fetch(t0 + kTT);
     constexpr int R = PF + 1;
     float2 xd[R];
@@ -1427,16 +1466,20 @@ __device__ __forceinline__ void bwd_agg_body(const BwdArgs<T>& p, const int b) {
     bool alive = false;
 #pragma unroll
     for (int j = 0; j < SPL; ++j) alive = alive || (live[j] && P[j] != 0.0f);
-    if (!barrier_any<kBwdWaves>(alive, s_alive[buf]) || !more) break;
+    vote = barrier_or<kBwdWaves>((__ballot(alive) != 0 ? 1 : 0) | (pflush ? 2 : 0), s_alive[buf]);
+    if (vote != 1 || !more) break;
   }
-  const int64_t o = (int64_t)b * p.nseg + seg;
+  const bool stop = (vote & 2) != 0;
+  const int64_t o = (int64_t)b * p.nseg * p.asub + seg;
 #pragma unroll
   for (int j = 0; j < SPL; ++j) {
     if (live[j]) {
-      p.agg_G[(o * N + SPL * g + j) * D + d] = G[j];
-      p.agg_P[(o * N + SPL * g + j) * D + d] = P[j];
+      p.agg_G[(o * N + SPL * g + j) * D + d] = stop ? 0.0f : G[j];
+      p.agg_P[(o * N + SPL * g + j) * D + d] = stop ? 0.0f : P[j];
     }
   }
+  if (fl && (stop || (vote & 1) == 0) && tid == 0)
+    __hip_atomic_store(fl, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // As ssm_fwd_agg_kernel: rows of p0 below rows0, rows of p1 above.
@@ -1525,6 +1568,7 @@ struct Shape {
   int spl_f, spl_b;           // states per lane of the forward and backward kernels
   bool epi;                   // skip / gate epilogue fused
   int seg_len, nseg;          // time segments per row
+  int asub, nagg;             // aggregate walks per segment, and in a row (nseg * asub)
   int ldy, ldz;               // row strides of y / dy and of z
   int ldbc;                   // row stride of B, C, dB, dC
 };
@@ -1538,6 +1582,7 @@ constexpr int kFillWaves = 2048;
 constexpr int kMaxGridY = 65535;  // grid.y limit: batch rows (or both calls' rows of a pair) per launch
 constexpr int kMinAutoSeg = 512;
 constexpr int kMaxSeg = 1024;
+constexpr int kMinPiece = 16384;  // steps of an aggregate piece
 
 void choose_segments(const ssm_desc_t* desc, Shape* s) {
   int64_t want = desc->segments;
@@ -1550,6 +1595,22 @@ void choose_segments(const ssm_desc_t* desc, Shape* s) {
   len = (len + kTT - 1) / kTT * kTT;  // segments start on forward tiles
   s->seg_len = (int)len;
   s->nseg = (int)((s->L + len - 1) / len);
+  // The aggregate passes walk every segment but one, with 4 forward waves per
+  // 64 channels: for long rows of few channels that is under one wave per
+  // SIMD, and a walk that does not decay to 0 crosses the whole segment.  Each
+  // segment's walk is then split in 2, 4 or 8 pieces of at least kMinPiece
+  // steps; the main passes fold the pieces' carries in order, a few FMAs each.
+  // A piece walks until its own decay product flushes (or a flag stops it), so
+  // for walks a little longer than a piece the pieces only add reads: pieces
+  // pay where walks can run far beyond kMinPiece steps.
+  s->asub = 1;
+  if (s->nseg > 1) {
+    const int64_t awaves = (int64_t)s->B * s->ncb * (s->nseg - 1) * kFwdWaves;
+    while (s->asub < 8 && awaves * s->asub < kFillWaves && s->seg_len % (2 * s->asub * kTT) == 0 &&
+           s->seg_len / (2 * s->asub) >= kMinPiece)
+      s->asub *= 2;
+  }
+  s->nagg = s->nseg * s->asub;
 }
 
 int validate(const ssm_desc_t* desc, Shape* s) {
@@ -1636,12 +1697,15 @@ size_t ypre_bytes(const ssm_desc_t* desc, const Shape& s) {
   return (n + 15) / 16 * 16;  // the buffer stays a whole number of floats (and 16-byte granules)
 }
 
-// Per-segment aggregates of a time-split scan: [B][nseg][N][D] states (or
-// adjoint carries) then [B][nseg][N][D] decay products.  None for one segment.
-size_t agg_floats(const Shape& s) { return s.nseg > 1 ? (size_t)2 * s.B * s.nseg * s.N * s.D : 0; }
+// Aggregates of a time-split scan, per piece (asub per segment):
+// [B][nseg * asub][N][D] states (or adjoint carries) then [B][nseg * asub][N][D]
+// decay products.  None for one segment.
+size_t agg_floats(const Shape& s) { return s.nseg > 1 ? (size_t)2 * s.B * s.nagg * s.N * s.D : 0; }
+// The pieces' end flags, [B][nseg * asub][ncb] ints after the aggregates (asub > 1)
+size_t flag_ints(const Shape& s) { return s.asub > 1 ? (size_t)s.B * s.nagg * s.ncb : 0; }
 
 struct WsLayout {
-  size_t dB, dC, dA, dD, ddt, aggG, aggP, total;  // float offsets
+  size_t dB, dC, dA, dD, ddt, aggG, aggP, flg, total;  // float offsets
 };
 
 WsLayout ws_layout(const Shape& s, bool bcast) {
@@ -1654,8 +1718,9 @@ WsLayout ws_layout(const Shape& s, bool bcast) {
   w.dD = w.dA + parts * s.D * s.N;
   w.ddt = w.dD + parts * s.D;
   w.aggG = w.ddt + (bcast ? (size_t)s.ncb * s.B * s.L : 0);
-  w.aggP = w.aggG + (s.nseg > 1 ? parts * s.N * s.D : 0);
-  w.total = w.aggG + agg_floats(s);
+  w.aggP = w.aggG + (s.nseg > 1 ? (size_t)s.B * s.nagg * s.N * s.D : 0);
+  w.flg = w.aggG + agg_floats(s);
+  w.total = w.flg + flag_ints(s);
   return w;
 }
 
@@ -1675,13 +1740,15 @@ FwdArgs<T> fwd_args(const ssm_desc_t* desc, const Shape& s, const void* u, const
   a.ckpt = ckpt;
   a.ypre = ckpt != nullptr && (desc->flags & SSM_GATE) ? reinterpret_cast<T*>(ckpt + ckpt_floats(s)) : nullptr;
   a.agg_H = static_cast<float*>(workspace);
-  a.agg_P = a.agg_H + (s.nseg > 1 ? (size_t)s.B * s.nseg * s.N * s.D : 0);
+  a.agg_P = a.agg_H + (s.nseg > 1 ? (size_t)s.B * s.nagg * s.N * s.D : 0);
+  a.aflag = s.asub > 1 ? reinterpret_cast<int*>(a.agg_H + agg_floats(s)) : nullptr;
   a.L = s.L;
   a.D = s.D;
   a.N = s.N;
   a.nblk = s.nblk;
   a.seg_len = s.seg_len;
   a.nseg = s.nseg;
+  a.asub = s.asub;
   a.ldy = s.ldy;
   a.ldz = s.ldz;
   a.ldbc = s.ldbc;
@@ -1697,15 +1764,34 @@ bool fwd_vec(const ssm_desc_t* desc, const Shape& s, const FwdArgs<T>& a) {
          reinterpret_cast<uintptr_t>(a.delta) % (4 * sizeof(T)) == 0;
 }
 
+// Zeroes n ints at f0 and, when it differs, at f1: the pieces' end flags of
+// one or two calls, before their aggregate pass (a kernel, not a memset, so
+// the sequence can be captured in a graph).
+__global__ void clear_flags_kernel(int* f0, int* f1, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) {
+    f0[i] = 0;
+    if (f1 != f0) f1[i] = 0;
+  }
+}
+
+int launch_clear_flags(hipStream_t st, const Shape& s, int* f0, int* f1) {
+  if (s.asub <= 1) return SSM_OK;
+  const int64_t n = (int64_t)flag_ints(s);
+  hipLaunchKernelGGL(clear_flags_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, f0, f1, n);
+  return hip_check(hipGetLastError(), "aggregate flag clear launch");
+}
+
 // Aggregates of every segment but the last (s.nseg > 1): rows of a0, and with
 // a pair (rows = 2 * s.B) the rows of a1 in the same launch.
 template <typename T>
 int launch_fwd_agg(hipStream_t st, const Shape& s, const FwdArgs<T>& a0, const FwdArgs<T>& a1, int rows) {
+  if (int rc = launch_clear_flags(st, s, a0.aflag, a1.aflag)) return rc;
   if (!dispatch_spl<4, 8>(s.spl_f, false, [&](auto spl, auto) {
         constexpr int S = decltype(spl)::value;
         auto go = [&](auto sp) {
           constexpr bool SP = decltype(sp)::value;
-          hipLaunchKernelGGL((ssm_fwd_agg_kernel<S, SP, T>), dim3(s.ncb, rows, s.nseg - 1), dim3(kWave * kFwdWaves),
+          hipLaunchKernelGGL((ssm_fwd_agg_kernel<S, SP, T>), dim3(s.ncb, rows, (s.nseg - 1) * s.asub), dim3(kWave * kFwdWaves),
                              0, st, a0, a1, s.B);
         };
         if (a0.flags & SSM_DELTA_SOFTPLUS) go(std::true_type{}); else go(std::false_type{});
@@ -1772,6 +1858,7 @@ BwdArgs<T> bwd_args(const ssm_desc_t* desc, const Shape& s, const void* u, const
   a.ws_ddt = ws + wl.ddt;
   a.agg_G = ws + wl.aggG;
   a.agg_P = ws + wl.aggP;
+  a.aflag = s.asub > 1 ? reinterpret_cast<int*>(ws + wl.flg) : nullptr;
   a.Bt = s.B;
   a.L = s.L;
   a.D = s.D;
@@ -1780,6 +1867,7 @@ BwdArgs<T> bwd_args(const ssm_desc_t* desc, const Shape& s, const void* u, const
   a.ncb = s.ncb;
   a.seg_len = s.seg_len;
   a.nseg = s.nseg;
+  a.asub = s.asub;
   a.ldy = s.ldy;
   a.ldz = s.ldz;
   a.ldbc = s.ldbc;
@@ -1792,10 +1880,11 @@ BwdArgs<T> bwd_args(const ssm_desc_t* desc, const Shape& s, const void* u, const
 // and with a pair (rows = 2 * s.B) the rows of a1 in the same launch.
 template <typename T>
 int launch_bwd_agg(hipStream_t st, const Shape& s, const BwdArgs<T>& a0, const BwdArgs<T>& a1, int rows) {
+  if (int rc = launch_clear_flags(st, s, a0.aflag, a1.aflag)) return rc;
   if (!dispatch_spl<2, 4>(s.spl_b, s.epi, [&](auto spl, auto epi) {
         constexpr int S = decltype(spl)::value;
         constexpr bool E = decltype(epi)::value;
-        hipLaunchKernelGGL((ssm_bwd_agg_kernel<S, E, T>), dim3(s.ncb, rows, s.nseg - 1), dim3(kWave * kBwdWaves), 0,
+        hipLaunchKernelGGL((ssm_bwd_agg_kernel<S, E, T>), dim3(s.ncb, rows, (s.nseg - 1) * s.asub), dim3(kWave * kBwdWaves), 0,
                            st, a0, a1, s.B);
       }))
     return fail(SSM_ERR_UNSUPPORTED, "no kernel variant for this shape");
@@ -1939,7 +2028,7 @@ size_t ssm_fwd_workspace_bytes(const ssm_desc_t* desc) {
   g_last_error.clear();
   Shape s;
   if (validate(desc, &s)) return 0;
-  return agg_floats(s) * sizeof(float);
+  return agg_floats(s) * sizeof(float) + flag_ints(s) * sizeof(int);
 }
 
 size_t ssm_bwd_workspace_bytes(const ssm_desc_t* desc) {

@@ -61,7 +61,11 @@ static void size_queries() {
     const size_t bw = ssm_bwd_workspace_bytes(&d);
     check(ck == size_t(d.batch) * ((d.seqlen + 15) / 16) * d.dstate * d.dim * 4, "checkpoint size formula");
     check(bw > 0 && std::strlen(ssm_last_error()) == 0, "valid desc: workspace size, no error");
-    check(fw % (2 * size_t(d.batch) * d.dstate * d.dim * 4) == 0, "forward workspace holds whole segments");
+    // whole aggregates (end state and decay product per state and channel), and with
+    // pieces an int flag per 64-channel block each
+    const size_t per = 2 * size_t(d.batch) * d.dstate * d.dim * 4;
+    const size_t per_flagged = per + size_t(d.batch) * ((d.dim + 63) / 64) * 4;
+    check(fw % per == 0 || fw % per_flagged == 0, "forward workspace holds whole segments");
   }
 }
 

@@ -74,8 +74,16 @@ def test_time_split_workspace_follows_the_segment_rule():
     # long-sequence shapes split in time: B*ceil(D/32)*ceil(N/4) waves, 2048 slots
     # config 3 (1 x 1M x 1024): 128 waves -> 16 segments; config 2 per direction: 256 -> 8
     per_seg = lambda B, N, D: B * 2 * N * D * 4  # end state and decay product per (row, state, channel)
-    assert fwd_ws(batch=1, seqlen=1 << 20, dim=1024, dstate=16) == 16 * per_seg(1, 16, 1024)
+    # each segment's aggregate walk is split into asub pieces while the walks of
+    # every segment but one leave fewer than 2048 forward waves (4 per 64
+    # channels) and a piece stays >= 16384 steps; with pieces, each (row, piece,
+    # 64-channel block) also holds an int flag after the aggregates.
+    # config 3: 960 waves, 65536-step segments -> 4 pieces; config 2: 16384-step
+    # segments -> none
+    per_piece = lambda B, N, D: per_seg(B, N, D) + B * ((D + 63) // 64) * 4
+    assert fwd_ws(batch=1, seqlen=1 << 20, dim=1024, dstate=16) == 16 * 4 * per_piece(1, 16, 1024)
     assert fwd_ws(batch=4, seqlen=131072, dim=512, dstate=16) == 8 * per_seg(4, 16, 512)
+    assert fwd_ws(batch=1, seqlen=65536, dim=40, dstate=8, segments=2) == 2 * 2 * per_piece(1, 8, 40)
     # segments never shorter than 512 steps when chosen automatically
     assert fwd_ws(batch=1, seqlen=1024, dim=32, dstate=4) == 2 * per_seg(1, 4, 32)
     assert fwd_ws(batch=1, seqlen=511, dim=32, dstate=4) == 0

@@ -40,6 +40,8 @@ def _close(name, got, ref, rtol=1e-4, atol=1e-5):
 
 
 def _nseg(desc_shape, nbytes_fwd_ws):
+    """Time segments per row the forward workspace holds aggregates for (shapes whose segments
+    are walked whole: one end state and decay product per segment, state and channel)."""
     B, L, D, N = desc_shape
     return nbytes_fwd_ws // (2 * B * N * D * 4) if nbytes_fwd_ws else 1
 

@@ -100,6 +100,50 @@ def test_automatic_split_of_a_long_row():
         _close(f"d{k}", g[k], gr[k])
 
 
+@pytest.mark.parametrize("decay,flags", [
+    ("fast", ()),                                   # products flush within a piece: the pieces' flags
+    ("slow", ("reverse", "complement", "skip")),    # no flush: every piece walked whole and folded
+])
+def test_aggregate_pieces_match_oracle(decay, flags):
+    from selectssm_amd import _lib as L
+
+    # 2 segments of 32768 steps, each aggregate walked in 2 pieces of 16384 (with one int
+    # flag per piece and 64-channel block), 40 channels: a ragged channel block
+    shape = (1, 65536, 40, 8)
+    per_piece = 2 * 8 * 40 * 4 + 4
+    assert L.size_query(L.lib().ssm_fwd_workspace_bytes, L.make_desc(*shape, segments=2)) == 2 * 2 * per_piece
+    print(f"pieces decay={decay} flags={flags} shape={shape}", flush=True)
+    inp = make_inputs(*shape, seed=6)
+    if decay == "slow":
+        # delta about 2e-4: the sum of a*delta over any piece stays above -53 (seed 6), so no
+        # product reaches 2^-126 = e^-87.3 (with the synthetic delta the slowest state
+        # flushes after some 4300 steps)
+        inp["dt"] = (inp["dt"] * 0.01).astype(np.float32)
+    y, g = _run(inp, flags, segments=2)
+    yr, gr = _oracle(inp, flags)
+    got = dict(y=y, **{f"d{k}": g[k] for k in ("u", "dt", "A", "B", "C", "D")})
+    ref = dict(y=yr, **{f"d{k}": gr[k] for k in ("u", "dt", "A", "B", "C", "D")})
+    names = ["y", "du", "ddt", "dA", "dB", "dC"] + (["dD"] if "skip" in flags else [])
+    if decay == "fast":
+        at = lambda r: ATOL * max(1.0, float(np.abs(r).max()))
+        for k in names:
+            _close(k, got[k], ref[k], RTOL, at(ref[k]))
+        return
+    # With some 5000 steps of memory the fp32 adjoint sums round at about 1e-5 of the
+    # largest gradient: each result within 1e-4 of its largest reference value, and no
+    # farther from the oracle than the unsplit run of the same inputs (the fold of the
+    # pieces' carries adds no error of its own)
+    y1, g1 = _run(inp, flags, segments=1)
+    one = dict(y=y1, **{f"d{k}": g1[k] for k in ("u", "dt", "A", "B", "C", "D")})
+    for k in names:
+        scale = max(1.0, float(np.abs(ref[k]).max()))
+        _close(k, got[k], ref[k], 0.0, 1e-4 * scale)
+        err = lambda t: float(np.abs(t.detach().double().cpu().numpy() - np.asarray(ref[k], np.float64)).max())
+        e2, e1 = err(got[k]), err(one[k])
+        print(f"  {k}: max err split {e2:.3e}, unsplit {e1:.3e}, max |ref| {scale:.3e}", flush=True)
+        assert e2 <= 2.0 * e1 + 1e-6 * scale, (k, e2, e1)
+
+
 def test_split_and_unsplit_agree():
     inp = make_inputs(2, 4096, 96, 16, seed=4)
     y1, g1 = _run(inp, ("skip", "gate"), segments=1)
@@ -181,7 +225,8 @@ def test_config3_split_is_automatic():
     from selectssm_amd import _lib as L
 
     d = L.make_desc(*SHAPE3)
-    assert L.size_query(L.lib().ssm_fwd_workspace_bytes, d) == 16 * 32 * 1024 * 4
+    # 16 segments x 4 aggregate pieces, P and H per piece and an int flag per 64 channels
+    assert L.size_query(L.lib().ssm_fwd_workspace_bytes, d) == 16 * 4 * (32 * 1024 + 16) * 4
 
 
 def test_config3_exact_linearity(inputs3, split3):
