@@ -2,8 +2,9 @@
 caller-supplied workspace (for callers that cannot allocate).  Called through the
 C ABI, it must give ssm_bwd's results bit for bit, on two calls in a row with
 the second on a smaller input (the scratch keeps the first call's contents),
-(the refusal of a desc whose workspace exceeds the scratch is a CPU test in
-test_abi.py)."""
+and on two calls of one pieces-split shape whose first leaves aggregate flags
+in the scratch that the second must not see (the refusal of a desc whose
+workspace exceeds the scratch is a CPU test in test_abi.py)."""
 import ctypes
 
 import pytest
@@ -56,3 +57,29 @@ def test_static_scratch_backward_equals_ssm_bwd(flags):
             if a is not None:
                 assert torch.equal(a, b), name
 
+
+
+def test_static_scratch_clears_the_pieces_flags():
+    # A time split whose aggregates are walked in pieces (2 segments of 32768 steps, 2
+    # pieces each).  The first call's fast decays flush inside a piece and raise its end
+    # flag in the scratch; the second call, same shape and so same flag slots, decays too
+    # slowly for any flag, so a flag left over from the first would stop its pieces and
+    # change its gradients: both calls must equal ssm_bwd bit for bit.
+    lib = L.lib()
+    shape, segments = (1, 65536, 40, 8), 2
+    for decay in ("fast", "slow"):
+        print(f"ssm_bwd_static pieces decay={decay} shape={shape} segments={segments}", flush=True)
+        x = make_inputs_gpu(*shape, seed=7)
+        if decay == "slow":
+            x["dt"] = (x["dt"] * 0.01).contiguous()  # no product reaches 2^-126 within a piece
+        desc = _desc(x["u"], x["dt"], x["A"], _flags(False, False, False, False), segments)
+        assert 0 < L.size_query(lib.ssm_bwd_workspace_bytes, desc) <= SCRATCH
+        _, ck = scan_fwd(x["u"], x["dt"], x["A"], x["B"], x["C"], None, None, False, False, segments=segments)
+        ref = scan_bwd(x["u"], x["dt"], x["A"], x["B"], x["C"], None, None, ck, x["g"], False, False,
+                       segments=segments)
+        got = _static_bwd(x, None, None, ck, x["g"], False, False, segments)
+        torch.cuda.synchronize()
+        for name, a, b in zip(("du", "ddelta", "dA", "dB", "dC", "dD", "dz"), ref, got):
+            assert (a is None) == (b is None), name
+            if a is not None:
+                assert torch.equal(a, b), name
