@@ -550,14 +550,15 @@ __global__ void __launch_bounds__(kWave* kFwdWaves, 1) ssm_fwd_kernel(FwdArgs<T>
 // steps add exact zeros and the walk stops there: with decaying states only
 // the last few thousand steps of a long segment are read.
 //
-// With asub > 1 the segment is walked in asub pieces (workgroup z: piece
-// index), each into its own (H, P); the main pass folds them in order.  When
+// With asub > 1 the segment is walked in asub pieces (workgroup z selects the
+// piece), each into its own (H, P); the main pass folds them in order.  When
 // a piece's products all end at 0 it raises its flag, and the piece before
 // it in the segment, whose contributions reach the segment's end only through
 // those products (an exact 0 times a finite value), stops and writes H = P = 0:
 // the fold then gives the same floats.  The pieces at the segments' ends are
-// dispatched first, so with fast decays the earlier ones mostly stop after
-// one tile instead of each walking until its own products flush.
+// dispatched first; with fast decays an earlier piece, polling once per tile,
+// then stops as soon as the piece after it has flushed instead of walking
+// until its own products flush.
 template <int SPL, bool SP, typename T>
 __device__ __forceinline__ void fwd_agg_body(const FwdArgs<T>& p, const int b) {
   constexpr int NS = 4 * SPL;
