@@ -3,7 +3,8 @@ one call, the time-split aggregate passes of both in one launch.  Each result
 must equal the single ssm_fwd / ssm_bwd call bit for bit (the pair keeps each
 call's own time segments), with and without a time split, for every epilogue
 flag, when the two calls need different kernel variants (no joint launch),
-for bf16 I/O and for N = 32."""
+for bf16 I/O, for N = 32 and for segments long enough to be aggregated in
+pieces."""
 import pytest
 
 torch = pytest.importorskip("torch")
@@ -22,6 +23,9 @@ CASES = [
     ((2, 1024, 64, 16), 4, torch.float32, "mixed"),
     ((2, 1024, 128, 16), 4, torch.bfloat16, "epi"),
     ((1, 1024, 64, 32), 4, torch.float32, "epi"),
+    # 2 segments of 32768 steps whose aggregates are walked in 2 pieces each: the joint
+    # aggregate launch clears both calls' piece flags (each in its own workspace)
+    ((1, 65536, 40, 8), 2, torch.float32, "plain"),
 ]
 
 
