@@ -102,6 +102,7 @@ def test_automatic_split_of_a_long_row():
 
 @pytest.mark.parametrize("decay,flags", [
     ("fast", ()),                                   # products flush within a piece: the pieces' flags
+    ("fast", ("reverse", "complement", "skip", "gate")),  # the gated aggregate variant (dy times the gate)
     ("slow", ("reverse", "complement", "skip")),    # no flush: every piece walked whole and folded
 ])
 def test_aggregate_pieces_match_oracle(decay, flags):
@@ -121,9 +122,10 @@ def test_aggregate_pieces_match_oracle(decay, flags):
         inp["dt"] = (inp["dt"] * 0.01).astype(np.float32)
     y, g = _run(inp, flags, segments=2)
     yr, gr = _oracle(inp, flags)
-    got = dict(y=y, **{f"d{k}": g[k] for k in ("u", "dt", "A", "B", "C", "D")})
-    ref = dict(y=yr, **{f"d{k}": gr[k] for k in ("u", "dt", "A", "B", "C", "D")})
-    names = ["y", "du", "ddt", "dA", "dB", "dC"] + (["dD"] if "skip" in flags else [])
+    got = dict(y=y, **{f"d{k}": g[k] for k in ("u", "dt", "A", "B", "C", "D", "z")})
+    ref = dict(y=yr, **{f"d{k}": gr[k] for k in ("u", "dt", "A", "B", "C", "D", "z")})
+    names = (["y", "du", "ddt", "dA", "dB", "dC"] + (["dD"] if "skip" in flags else [])
+             + (["dz"] if "gate" in flags else []))
     if decay == "fast":
         at = lambda r: ATOL * max(1.0, float(np.abs(r).max()))
         for k in names:
@@ -134,7 +136,7 @@ def test_aggregate_pieces_match_oracle(decay, flags):
     # farther from the oracle than the unsplit run of the same inputs (the fold of the
     # pieces' carries adds no error of its own)
     y1, g1 = _run(inp, flags, segments=1)
-    one = dict(y=y1, **{f"d{k}": g1[k] for k in ("u", "dt", "A", "B", "C", "D")})
+    one = dict(y=y1, **{f"d{k}": g1[k] for k in ("u", "dt", "A", "B", "C", "D", "z")})
     for k in names:
         scale = max(1.0, float(np.abs(ref[k]).max()))
         _close(k, got[k], ref[k], 0.0, 1e-4 * scale)
@@ -142,6 +144,22 @@ def test_aggregate_pieces_match_oracle(decay, flags):
         e2, e1 = err(got[k]), err(one[k])
         print(f"  {k}: max err split {e2:.3e}, unsplit {e1:.3e}, max |ref| {scale:.3e}", flush=True)
         assert e2 <= 2.0 * e1 + 1e-6 * scale, (k, e2, e1)
+
+
+def test_aggregate_pieces_bf16():
+    # bf16 I/O through the pieces (2 segments of 2 pieces), skip and gate fused; the oracle
+    # runs on the bf16-rounded inputs, tolerances as for the other bf16 time splits
+    shape = (1, 65536, 40, 8)
+    print(f"pieces bf16 shape={shape}", flush=True)
+    inp = make_inputs(*shape, seed=9)
+    bf = {k: (torch.from_numpy(v).to(torch.bfloat16).float().numpy().astype(np.float64)
+              if k in ("u", "dt", "B", "C", "z", "g") else v) for k, v in inp.items()}
+    y, g = _run(bf, ("skip", "gate"), dtype=torch.bfloat16, segments=2)
+    yr, gr = _oracle(bf, ("skip", "gate"))
+    at = lambda r: 2e-2 * max(1.0, float(np.abs(r).max()))
+    _close("y", y, yr, 2e-2, at(yr))
+    for k in ("u", "dt", "A", "B", "C", "D", "z"):
+        _close(f"d{k}", g[k], gr[k], 2e-2, at(gr[k]))
 
 
 def test_split_and_unsplit_agree():
