@@ -26,6 +26,8 @@ SHAPES = [
     (2, 33, 130, 5),      # N not a multiple of the per-wave state count
     (1, 37, 64, 32),      # N = 32
     (3, 1, 65, 16),       # L = 1
+    (2, 50, 1, 1),        # D = 1, N = 1: one live channel and one live state per workgroup
+    (1, 45, 3, 32),       # N = 32 over 3 channels
     # config-1 width with more rows than fill the chip once (9 x 32 channel blocks)
     (9, 40, 2048, 16),
     (9, 37, 2046, 13),
