@@ -146,6 +146,25 @@ def test_aggregate_pieces_match_oracle(decay, flags):
         assert e2 <= 2.0 * e1 + 1e-6 * scale, (k, e2, e1)
 
 
+def test_aggregate_pieces_ragged_last_segment():
+    from selectssm_amd import _lib as L
+
+    # L = 70000 in 2 forced segments: 35008 steps (whole 32-step tiles), then 34992; each
+    # aggregate walked in 2 pieces of 17504, so the backward's last piece ends at L, 16 steps
+    # short of its length
+    shape = (1, 70000, 40, 8)
+    assert L.size_query(L.lib().ssm_fwd_workspace_bytes, L.make_desc(*shape, segments=2)) == 4 * (2 * 8 * 40 + 1) * 4
+    print(f"pieces ragged shape={shape}", flush=True)
+    inp = make_inputs(*shape, seed=10)
+    flags = ("reverse", "skip")
+    y, g = _run(inp, flags, segments=2)
+    yr, gr = _oracle(inp, flags)
+    at = lambda r: ATOL * max(1.0, float(np.abs(r).max()))
+    _close("y", y, yr, RTOL, at(yr))
+    for k in ("u", "dt", "A", "B", "C", "D"):
+        _close(f"d{k}", g[k], gr[k], RTOL, at(gr[k]))
+
+
 def test_aggregate_pieces_bf16():
     # bf16 I/O through the pieces (2 segments of 2 pieces), skip and gate fused; the oracle
     # runs on the bf16-rounded inputs, tolerances as for the other bf16 time splits
